@@ -1,0 +1,192 @@
+"""MoE-layer benchmark on one MI355X (contract: one JSON line on stdout).
+
+Workload: one Qwen1.5-MoE-A2.7B-shaped MoE block,
+W4A16 routed experts (60 x [1408 x 2048], top-4, Q4 group-128 with FP32
+scales) plus the BF16 shared expert (5632) and its sigmoid gate, decode batch
+1, seeded synthetic weights N(0, 0.02). A step is one MoE block call on one
+token: router, top-k, permutation, routed gate/up/SiLU/down, shared expert,
+combine. R distinct layer instances (R x bytes >= 1 GiB) are rotated so that
+the 256 MB MALL cannot serve the weights; the R calls are captured in one HIP
+graph, which the timed region replays.
+
+``value`` is microseconds per token per MoE layer (lower is better). The
+roofline is HBM: algorithmic bytes = weight bytes one call must read (each
+selected expert once + router + shared expert + shared gate).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "uma-qmoe_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2"])
+    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--rotate-bytes", type=float, default=1.1e9)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_baseline(shape, seconds: float):
+    """The oracle (reference CPU correctness path restated) on the host cores:
+    transient dequantization every call, FP32 FFN, BF16 index_add_, BF16 shared
+    expert. Bounded: calls repeat until ~``seconds`` of work is done."""
+    import torch
+
+    from oracle import moe as om
+    from uma_qmoe_amd import synthetic as syn
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    layer = syn.build_experts(shape, seed=syn.SEED + 1)
+    dense = syn.build_dense(shape, seed=syn.SEED + 1)
+    reader = syn.DeviceLayerReader({0: layer})
+    lay = {"router": dense.router, "top_k": shape.top_k, "num_experts": shape.num_experts,
+           "shared_gate": dense.shared_gate, "shared_up": dense.shared_up, "shared_down": dense.shared_down,
+           "shared_expert_gate": dense.shared_expert_gate}
+    x = syn.hidden_states(shape, 1)
+    for _ in range(2):
+        om.qwen_block(x, lay, reader, 0)
+    times = []
+    start = time.perf_counter()
+    while time.perf_counter() - start < seconds or len(times) < 5:
+        t0 = time.perf_counter_ns()
+        om.qwen_block(x, lay, reader, 0)
+        times.append((time.perf_counter_ns() - t0) / 1e3)
+        if len(times) >= 200:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round(med, 1),
+        "unit": "us/token",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"median of {len(times)} single-token {shape.name} block calls (oracle, dequantize per call)",
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        return 2
+    import torch
+
+    from uma_qmoe_amd import synthetic as syn
+    from uma_qmoe_amd.native_backend import load_native_extension
+
+    _platform, ext = load_native_extension()
+    dev = torch.device("cuda:0")
+    shape = syn.CONFIGS[args.config]
+    t = args.tokens
+
+    # R distinct instances so the working set exceeds the MALL.
+    probe = syn.build_experts(shape, device=dev, seed=syn.SEED)
+    dense0 = syn.build_dense(shape, device=dev, seed=syn.SEED)
+    per_layer_total = probe.device_storage_bytes + sum(
+        v.numel() * v.element_size() for v in (dense0.router, dense0.shared_gate, dense0.shared_up,
+                                               dense0.shared_down, dense0.shared_expert_gate) if v is not None)
+    r_inst = max(1, math.ceil(args.rotate_bytes / per_layer_total))
+    layers = [probe] + [syn.build_experts(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
+    denses = [dense0] + [syn.build_dense(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
+    x = syn.hidden_states(shape, t, device=dev)
+    ws = ext._workspace(dev, t, shape.hidden, shape.intermediate, shape.shared_intermediate, shape.num_experts,
+                        shape.top_k)
+    outs = [torch.empty((t, shape.hidden), dtype=torch.bfloat16, device=dev) for _ in range(r_inst)]
+
+    def run_all():
+        res = []
+        for i in range(r_inst):
+            res.append(ext.moe_layer(layers[i], denses[i], x, shape.top_k, out=outs[i], workspace=ws))
+        return res
+
+    # eager warm-up, then capture the R calls in one graph
+    for _ in range(2):
+        results = run_all()
+    torch.cuda.synchronize()
+    distinct = [int(torch.unique(res[3]).numel()) for res in results]
+    algo_bytes = [syn.algorithmic_bytes(layers[i], denses[i], distinct[i]) for i in range(r_inst)]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run_all()
+    torch.cuda.synchronize()
+
+    replays = max(1, math.ceil(args.steps / r_inst))
+    warm = max(1, math.ceil(args.warmup / r_inst))
+    for _ in range(warm):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    samples = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(replays):
+            graph.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        samples.append(start.elapsed_time(stop))
+    ms_total = sorted(samples)[1]
+    steps = replays * r_inst
+    us_per_layer = ms_total * 1000.0 / steps
+    mean_bytes = sum(algo_bytes) / len(algo_bytes)
+    achieved = mean_bytes / (us_per_layer * 1e-6) / 1e9
+
+    line = {
+        "metric": "MoE layer us/token (Qwen1.5-MoE W4A16 block, decode batch 1) + achieved HBM GB/s",
+        "value": round(us_per_layer, 3),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm * r_inst,
+        "ms_per_step": round(us_per_layer / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w4a16 (q4 weights, bf16 activations, fp32 accumulate)",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) token)",
+        "config": {
+            "workload": f"{shape.name}: one MoE block (router + top-{shape.top_k} of {shape.num_experts} Q4 experts "
+                        f"I={shape.intermediate} + bf16 shared expert {shape.shared_intermediate}), H={shape.hidden}",
+            "tokens": t,
+            "rotated_instances": r_inst,
+            "parallelism": "single GPU",
+        },
+        "tokens_per_s": round(t / (us_per_layer * 1e-6), 1),
+        "algorithmic_bytes_per_call": int(mean_bytes),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(shape, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,276 @@
+"""GPU parity of the HIP kernels (through the C ABI) against the CPU oracle.
+
+Tolerances (north star): outputs rel-L2 <= 1e-2 and max-abs <= 2e-2 in bf16
+with fp32 accumulation; expert indices bit-exact given identical logits;
+permutation and index work bit-exact.
+"""
+
+from __future__ import annotations
+
+import sys
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import codec as oc
+from oracle import moe as om
+from uma_qmoe_amd import synthetic as syn
+from uma_qmoe_amd.native_backend import DenseBlock, DeviceExperts
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-2
+MAX_ABS = 2e-2
+DEV = "cuda:0"
+
+
+def note(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def to_dev(layer: DeviceExperts) -> DeviceExperts:
+    mv = lambda t: None if t is None else t.to(DEV)
+    return replace(layer, gate=mv(layer.gate), gate_scales=mv(layer.gate_scales), up=mv(layer.up),
+                   up_scales=mv(layer.up_scales), down=mv(layer.down), down_scales=mv(layer.down_scales))
+
+
+def dense_to_dev(d: DenseBlock) -> DenseBlock:
+    mv = lambda t: None if t is None else t.to(DEV)
+    return DenseBlock(mv(d.router), mv(d.shared_gate), mv(d.shared_up), mv(d.shared_down), mv(d.shared_expert_gate))
+
+
+def assert_close(got: torch.Tensor, ref: torch.Tensor, what: str, rel=REL_L2, mx=MAX_ABS):
+    r = om.rel_l2(got.cpu(), ref.cpu())
+    m = om.max_abs(got.cpu(), ref.cpu())
+    print(f"  {what}: rel_l2={r:.3e} max_abs={m:.3e}", flush=True)
+    assert torch.isfinite(got.float()).all(), what
+    assert r <= rel, f"{what}: rel-L2 {r}"
+    assert m <= mx, f"{what}: max-abs {m}"
+
+
+# ------------------------------------------------------------------ linear --
+@pytest.mark.parametrize("encoding", ["q4_group128", "q8_group128", "bf16_le"])
+@pytest.mark.parametrize("rows,n,k", [(1, 64, 2048), (3, 96, 1408), (7, 40, 768), (4, 256, 5632)])
+def test_linear_matches_oracle(hip_ext, encoding, rows, n, k):
+    note(f"linear {encoding} rows={rows} n={n} k={k}")
+    g = torch.Generator().manual_seed(rows * 1000 + n + k)
+    w = torch.randn(1, n, k, generator=g) * 0.02
+    data, scales = syn.encode_projection(w, encoding)
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+    if encoding == "q4_group128":
+        deq = oc.q4_dequantize(data.numpy().tobytes(), scales.numpy().tobytes(), (n, k))
+        got = hip_ext.q4_linear(x.to(DEV), data[0].to(DEV), scales[0].to(DEV), n, k, 128)
+    elif encoding == "q8_group128":
+        deq = oc.q8_dequantize(data.numpy().tobytes(), scales.numpy().tobytes(), (n, k))
+        got = hip_ext.q8_linear(x.to(DEV), data[0].to(DEV), scales[0].to(DEV), n, k, 128)
+    else:
+        deq = data[0].float().numpy()
+        got = hip_ext.bf16_linear(x.to(DEV), data[0].to(DEV))
+    ref = x.float() @ torch.from_numpy(deq).T
+    assert_close(got, ref, "linear", rel=4e-3, mx=1e-2)
+
+
+def test_q4_kernel_decodes_reserved_minus_eight(hip_ext):
+    """The codec rejects -8, but the kernel decodes full two's complement
+    (reference kernel src/uma_qmoe/native/packed_q4_kernel.cu:62-70)."""
+    note("q4 -8 decode")
+    n, k = 8, 256
+    rng = np.random.default_rng(0)
+    codes = rng.integers(-8, 8, size=(n, k)).astype(np.int8)
+    codes[:, 0] = -8
+    nib = (codes.astype(np.int16) & 0xF).astype(np.uint8).reshape(n, k // 2, 2)
+    packed = torch.from_numpy(nib[..., 0] | (nib[..., 1] << 4))
+    scales = torch.from_numpy(rng.uniform(0.001, 0.01, size=(n * k // 128,)).astype(np.float32))
+    x = torch.randn(2, k).to(torch.bfloat16)
+    got = hip_ext.q4_linear(x.to(DEV), packed.to(DEV), scales.to(DEV), n, k, 128)
+    deq = codes.astype(np.float32) * np.repeat(scales.numpy(), 128).reshape(n, k)
+    ref = x.float() @ torch.from_numpy(deq).T
+    assert_close(got, ref, "q4 with -8", rel=4e-3, mx=1e-2)
+
+
+def test_q4_groups_crossing_rows(hip_ext):
+    """Scale groups run over the flattened tensor (src/uma_qmoe/q4.py:146-159):
+    with K=64 and group 128 one group spans two rows."""
+    note("q4 flattened groups K=64")
+    n, k = 16, 64
+    w = torch.randn(n, k) * 0.02
+    packed, scales = oc.q4_quantize(w.numpy(), 128)
+    x = torch.randn(3, k).to(torch.bfloat16)
+    got = hip_ext.q4_linear(x.to(DEV), torch.frombuffer(bytearray(packed), dtype=torch.uint8).to(DEV),
+                            torch.frombuffer(bytearray(scales), dtype=torch.float32).to(DEV), n, k, 128)
+    ref = x.float() @ torch.from_numpy(oc.q4_dequantize(packed, scales, (n, k))).T
+    assert_close(got, ref, "crossing groups", rel=4e-3, mx=1e-2)
+
+
+# ----------------------------------------------------------------- routing --
+@pytest.mark.parametrize("t,k,e", [(1, 4, 60), (5, 8, 64), (512, 4, 60), (256, 8, 128), (33, 2, 256)])
+def test_route_permute_is_a_stable_sort(hip_ext, t, k, e):
+    note(f"permute t={t} k={k} e={e}")
+    g = torch.Generator().manual_seed(t + k + e)
+    idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(t)])
+    order, offsets = hip_ext.route_permute(idx.to(DEV), e)
+    flat = idx.reshape(-1)
+    assert torch.equal(order.cpu(), torch.argsort(flat, stable=True))
+    counts = torch.bincount(flat, minlength=e)
+    assert torch.equal(offsets.cpu(), torch.cat((torch.zeros(1, dtype=torch.int64), counts.cumsum(0))))
+
+
+def test_route_permute_drops_invalid_ids(hip_ext):
+    note("permute invalid ids")
+    idx = torch.tensor([[3, -1], [70, 3], [0, 5]])
+    order, offsets = hip_ext.route_permute(idx.to(DEV), 8)
+    assert order.cpu()[: int(offsets[-1])].tolist() == [4, 1, 2, 5]
+    assert offsets.cpu().tolist() == [0, 1, 1, 1, 3, 3, 4, 4, 4]
+
+
+@pytest.mark.parametrize("t,e,k", [(1, 60, 4), (7, 64, 8), (64, 128, 8)])
+def test_router_topk_bit_exact_given_logits(hip_ext, t, e, k):
+    note(f"router t={t} e={e} k={k}")
+    g = torch.Generator().manual_seed(e * t)
+    x = torch.randn(t, 2048, generator=g).to(torch.bfloat16)
+    w = (torch.randn(e, 2048, generator=g) * 0.02).to(torch.bfloat16)
+    logits, weights, indices = hip_ext.router_topk(x.to(DEV), w.to(DEV), k)
+    logits, weights, indices = logits.cpu(), weights.cpu(), indices.cpu()
+    ref_logits = torch.nn.functional.linear(x, w)
+    # logits: fp32 accumulation in a different order; at most one bf16 ulp apart
+    ulp = (ref_logits.float().abs() * 2.0 ** -7).clamp_min(2.0 ** -126)
+    assert ((logits.float() - ref_logits.float()).abs() <= ulp).all()
+    # selection is bit-exact given the kernel's own logits
+    assert torch.equal(indices, om.topk_ordered(logits, k))
+    probs = torch.softmax(logits.float(), -1).gather(-1, indices)
+    assert (weights.float() - probs).abs().max() <= 2.0 ** -8 * probs.max() + 1e-6
+
+
+def test_router_forced_ties_go_to_lower_id(hip_ext):
+    note("router forced ties")
+    g = torch.Generator().manual_seed(9)
+    base = (torch.randn(4, 2048, generator=g) * 0.02).to(torch.bfloat16)
+    w = base[torch.tensor([0, 1, 1, 2, 1, 3, 3, 0])]  # identical rows -> identical logits
+    x = torch.randn(16, 2048, generator=g).to(torch.bfloat16)
+    logits, _, indices = hip_ext.router_topk(x.to(DEV), w.to(DEV), 3)
+    assert torch.equal(indices.cpu(), om.topk_ordered(logits.cpu(), 3))
+    lc = logits.cpu().float()
+    for tt in range(16):
+        sel = indices.cpu()[tt].tolist()
+        for a, b in zip(sel, sel[1:]):
+            assert lc[tt, a] > lc[tt, b] or (lc[tt, a] == lc[tt, b] and a < b)
+
+
+# ----------------------------------------------------------------- experts --
+SMALL = syn.MoEShape("small_q4", 256, 8, 2, 128)
+
+
+def _routes(t, k, e, seed):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(t)])
+    w = torch.rand(t, k, generator=g).to(torch.bfloat16)
+    return idx, w
+
+
+@pytest.mark.parametrize("encoding", ["q4_group128", "q8_group128", "bf16_le"])
+@pytest.mark.parametrize("t", [1, 2, 3, 4, 9])
+def test_moe_forward_small(hip_ext, encoding, t):
+    note(f"moe_forward small {encoding} t={t}")
+    shape = replace(SMALL, encoding=encoding)
+    layer = syn.build_experts(shape, seed=t)
+    reader = syn.DeviceLayerReader({0: layer})
+    x = syn.hidden_states(shape, t, seed=t)
+    idx, w = _routes(t, shape.top_k, shape.num_experts, t)
+    got = hip_ext.moe_forward(to_dev(layer), x.to(DEV), idx.to(DEV), w.to(DEV))
+    ref = om.streaming_reference(x, idx, w, 0, reader, num_experts=shape.num_experts)
+    assert_close(got, ref, f"{encoding} t={t}")
+
+
+def test_moe_forward_edge_cases(hip_ext):
+    note("moe_forward edge cases")
+    layer = syn.build_experts(SMALL, seed=3)
+    dl = to_dev(layer)
+    reader = syn.DeviceLayerReader({0: layer})
+    x = syn.hidden_states(SMALL, 4, seed=3)
+    # duplicate expert inside one token
+    idx = torch.tensor([[2, 2], [1, 7], [7, 1], [0, 0]])
+    w = torch.tensor([[0.5, 0.25], [0.3, 0.7], [0.7, 0.3], [1.0, 0.0]]).to(torch.bfloat16)
+    got = hip_ext.moe_forward(dl, x.to(DEV), idx.to(DEV), w.to(DEV))
+    ref = om.streaming_reference(x, idx, w, 0, reader, num_experts=8)
+    assert_close(got, ref, "duplicates")
+    # zero weights -> zero output
+    z = hip_ext.moe_forward(dl, x.to(DEV), idx.to(DEV), torch.zeros_like(w).to(DEV))
+    assert torch.count_nonzero(z) == 0
+    # an invalid expert id contributes nothing (the reference kernel skips it)
+    bad = torch.tensor([[2, 99], [1, 7], [7, 1], [0, -3]])
+    got_bad = hip_ext.moe_forward(dl, x.to(DEV), bad.to(DEV), w.to(DEV))
+    keep = torch.tensor([[2, 0], [1, 7], [7, 1], [0, 0]])
+    wk = w.clone()
+    wk[0, 1] = 0
+    wk[3, 1] = 0
+    ref_bad = om.streaming_reference(x, keep, wk, 0, reader, num_experts=8)
+    assert_close(got_bad, ref_bad, "invalid ids")
+    # no tokens
+    empty = hip_ext.moe_forward(dl, x[:0].to(DEV), idx[:0].to(DEV), w[:0].to(DEV))
+    assert empty.shape == (0, SMALL.hidden)
+    # int32 indices and k=1
+    got1 = hip_ext.moe_forward(dl, x.to(DEV), idx[:, :1].to(torch.int32).to(DEV), w[:, :1].to(DEV))
+    ref1 = om.streaming_reference(x, idx[:, :1], w[:, :1], 0, reader, num_experts=8)
+    assert_close(got1, ref1, "k=1 int32")
+
+
+@pytest.mark.parametrize("name,t", [("c1", 1), ("c1", 3), ("c2", 1), ("c2", 4), ("c5", 1)])
+def test_moe_forward_benchmark_shapes(hip_ext, name, t):
+    shape = syn.CONFIGS[name]
+    note(f"moe_forward {shape.name} t={t}")
+    layer = syn.build_experts(shape, device=DEV)
+    reader = syn.DeviceLayerReader({0: layer})
+    x = syn.hidden_states(shape, t)
+    idx, w = _routes(t, shape.top_k, shape.num_experts, 17 + t)
+    got = hip_ext.moe_forward(layer, x.to(DEV), idx.to(DEV), w.to(DEV))
+    ref = om.streaming_reference(x, idx, w, 0, reader, num_experts=shape.num_experts)
+    assert_close(got, ref, f"{shape.name} t={t}")
+
+
+@pytest.mark.parametrize("name,t", [("c2", 1), ("c1", 1), ("c2", 3)])
+def test_moe_layer_matches_oracle_block(hip_ext, name, t):
+    """Whole block: router + routed + shared + sigmoid gate, one C-ABI call."""
+    shape = syn.CONFIGS[name]
+    note(f"moe_layer {shape.name} t={t}")
+    layer = syn.build_experts(shape, device=DEV)
+    dense = syn.build_dense(shape, device=DEV)
+    reader = syn.DeviceLayerReader({0: layer})
+    x = syn.hidden_states(shape, t)
+    out, logits, weights, indices = hip_ext.moe_layer(layer, dense, x.to(DEV), shape.top_k)
+    logits_c, weights_c, indices_c = logits.cpu(), weights.cpu(), indices.cpu()
+    assert torch.equal(indices_c, om.topk_ordered(logits_c, shape.top_k))
+    dense_c = DenseBlock(*(None if v is None else v.cpu() for v in (
+        dense.router, dense.shared_gate, dense.shared_up, dense.shared_down, dense.shared_expert_gate)))
+    ref_logits = torch.nn.functional.linear(x, dense_c.router)
+    ulp = (ref_logits.float().abs() * 2.0 ** -7).clamp_min(2.0 ** -126)
+    assert ((logits_c.float() - ref_logits.float()).abs() <= ulp).all()
+    lay = {"router": dense_c.router, "top_k": shape.top_k, "num_experts": shape.num_experts,
+           "shared_gate": dense_c.shared_gate, "shared_up": dense_c.shared_up, "shared_down": dense_c.shared_down,
+           "shared_expert_gate": dense_c.shared_expert_gate}
+    ref, *_ = om.qwen_block(x, lay, reader, 0, routes=(weights_c, indices_c))
+    assert_close(out, ref, f"{shape.name} block t={t}")
+
+
+@pytest.mark.parametrize("layer_index", [0, 16])
+def test_c3_stack_layer_encodings(hip_ext, layer_index):
+    """c3: routed BF16 (layers 0-15) and Q8 (layers 16-23) blocks with shared expert."""
+    shape = syn.c3_layer_shape(layer_index)
+    note(f"c3 layer {layer_index} {shape.encoding}")
+    layer = syn.build_experts(shape, layer=layer_index, device=DEV)
+    dense = syn.build_dense(shape, layer=layer_index, device=DEV)
+    reader = syn.DeviceLayerReader({layer_index: layer})
+    x = om.rmsnorm(syn.hidden_states(shape, 1, tag="c3"), 1e-6)
+    xr = hip_ext.rmsnorm(syn.hidden_states(shape, 1, tag="c3").to(DEV), 1e-6)
+    # rsqrt differs in the last fp32 bits; after the bf16 cast at most one ulp apart
+    assert ((xr.cpu().float() - x.float()).abs() <= x.float().abs() * 2.0 ** -7 + 1e-30).all()
+    out, logits, weights, indices = hip_ext.moe_layer(layer, dense, xr, shape.top_k)
+    dense_c = DenseBlock(*(None if v is None else v.cpu() for v in (
+        dense.router, dense.shared_gate, dense.shared_up, dense.shared_down, dense.shared_expert_gate)))
+    lay = {"router": dense_c.router, "top_k": shape.top_k, "num_experts": shape.num_experts,
+           "shared_gate": dense_c.shared_gate, "shared_up": dense_c.shared_up, "shared_down": dense_c.shared_down,
+           "shared_expert_gate": dense_c.shared_expert_gate}
+    ref, *_ = om.qwen_block(x, lay, reader, layer_index, routes=(weights.cpu(), indices.cpu()))
+    assert_close(out, ref, f"c3 layer {layer_index}")

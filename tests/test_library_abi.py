@@ -1,0 +1,46 @@
+"""The C-ABI library loads and exports every entry point include/uma_qmoe_hip.h
+declares (no compute calls: this runs without a GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+from uma_qmoe_amd import _native
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "uma_qmoe_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(uqm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_functions():
+    declared = declared_functions()
+    assert declared, "no uqm_* declarations found"
+    assert sorted(_native.SIGNATURES) == declared
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _native.library()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+    assert lib.uqm_abi_version() == _native.ABI_VERSION
+
+
+def test_workspace_query_is_host_only_and_validates():
+    lib = _native.library()
+    n = lib.uqm_moe_workspace_bytes(1, 2048, 1408, 5632, 60, 4)
+    assert n > 0 and n % 256 == 0
+    assert lib.uqm_moe_workspace_bytes(-1, 2048, 1408, 0, 60, 4) == 0
+    assert lib.uqm_moe_workspace_bytes(512, 2048, 1408, 5632, 60, 4) > n
+
+
+def test_struct_layouts_match_header():
+    # uqm_expert_weights: 2 x int32, 3 x int64, 6 pointers
+    assert ctypes.sizeof(_native.ExpertWeights) == 8 + 3 * 8 + 6 * 8
+    assert ctypes.sizeof(_native.LayerWeights) == ctypes.sizeof(_native.ExpertWeights) + 8 + 8 + 4 + 4 + 8 + 4 * 8

@@ -1,0 +1,446 @@
+// extern "C" entry points of libuma_qmoe_hip.so (declared in
+// include/uma_qmoe_hip.h). Each validates its arguments on the host, carves
+// the caller's workspace and enqueues kernels on the caller's stream.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <atomic>
+#include <string>
+
+#include "../../include/uma_qmoe_hip.h"
+#include "uqm_internal.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(UQM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return UQM_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int elems_per_chunk(int enc) { return enc == UQM_Q4 ? 32 : enc == UQM_Q8 ? 16 : 8; }
+
+size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+// Workspace carve-up shared by the size query and the entry points.
+struct Layout {
+  size_t counters, route_expert, route_order, expert_offsets, active_experts, logits, weights, indices, sg,
+      h_routed, y_routed, h_shared, y_shared, total;
+};
+
+Layout layout(int64_t T, int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k) {
+  Layout L{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align256(bytes);
+    return at;
+  };
+  const size_t R = static_cast<size_t>(T * k);
+  L.counters = take(256);
+  L.route_expert = take(4 * R);
+  L.route_order = take(4 * R);
+  L.expert_offsets = take(4 * (E + 1));
+  L.active_experts = take(4 * E);
+  L.logits = take(2 * static_cast<size_t>(T) * (E + 1));
+  L.weights = take(2 * R);
+  L.indices = take(8 * R);
+  L.sg = take(4 * static_cast<size_t>(T));
+  L.h_routed = take(2 * R * I);
+  L.y_routed = take(4 * R * H);
+  L.h_shared = take(2 * static_cast<size_t>(T) * Is);
+  L.y_shared = take(4 * static_cast<size_t>(T) * H);
+  L.total = off;
+  return L;
+}
+
+template <typename P>
+P* at(void* ws, size_t off) {
+  return reinterpret_cast<P*>(static_cast<unsigned char*>(ws) + off);
+}
+
+// Per-device verdict of the gfx950 check: 0 unknown, 1 gfx950, 2 other.
+std::atomic<int> g_device_ok[64];
+
+int check_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(UQM_ERR_HIP, "hipGetDevice failed");
+  if (dev >= 0 && dev < 64) {
+    const int v = g_device_ok[dev].load(std::memory_order_relaxed);
+    if (v == 1) return UQM_OK;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return fail(UQM_ERR_HIP, "hipGetDeviceProperties failed");
+  const bool ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+  if (dev >= 0 && dev < 64) g_device_ok[dev].store(ok ? 1 : 2, std::memory_order_relaxed);
+  if (!ok) return fail(UQM_ERR_DEVICE, "libuma_qmoe_hip requires gfx950, current device is %s", prop.gcnArchName);
+  return UQM_OK;
+}
+
+int check_matrix(int enc, int64_t K, int64_t group, const void* w, const float* s, const char* name) {
+  if (w == nullptr) return fail(UQM_ERR_ARGUMENT, "%s weights are NULL", name);
+  if (!aligned16(w)) return fail(UQM_ERR_ARGUMENT, "%s weights must be 16-byte aligned", name);
+  const int el = elems_per_chunk(enc);
+  if (K <= 0 || K % el != 0) return fail(UQM_ERR_ARGUMENT, "%s input features %lld must be a multiple of %d", name, (long long)K, el);
+  if (K % 8 != 0) return fail(UQM_ERR_ARGUMENT, "%s input features must be a multiple of 8", name);
+  if (enc != UQM_BF16) {
+    if (s == nullptr) return fail(UQM_ERR_ARGUMENT, "%s scales are NULL", name);
+    if (group <= 0 || group % el != 0)
+      return fail(UQM_ERR_ARGUMENT, "%s group size %lld must be a positive multiple of %d", name, (long long)group, el);
+  }
+  return UQM_OK;
+}
+
+int check_experts(const uqm_expert_weights* w) {
+  if (w == nullptr) return fail(UQM_ERR_ARGUMENT, "expert weights descriptor is NULL");
+  if (w->encoding != UQM_Q4 && w->encoding != UQM_Q8 && w->encoding != UQM_BF16)
+    return fail(UQM_ERR_ARGUMENT, "unsupported expert encoding %d", w->encoding);
+  if (w->num_experts <= 0 || w->num_experts > 256) return fail(UQM_ERR_ARGUMENT, "num_experts must be in [1, 256]");
+  if (w->hidden_size <= 0 || w->intermediate_size <= 0) return fail(UQM_ERR_ARGUMENT, "hidden and intermediate sizes must be positive");
+  int rc;
+  if ((rc = check_matrix(w->encoding, w->hidden_size, w->group_size, w->gate, w->gate_scales, "gate"))) return rc;
+  if ((rc = check_matrix(w->encoding, w->hidden_size, w->group_size, w->up, w->up_scales, "up"))) return rc;
+  if ((rc = check_matrix(w->encoding, w->intermediate_size, w->group_size, w->down, w->down_scales, "down"))) return rc;
+  return UQM_OK;
+}
+
+int check_lds(int enc, int64_t K, int nt) {
+  if (uqm::gemv_lds_bytes(enc, K, nt) > 64 * 1024)
+    return fail(UQM_ERR_ARGUMENT, "input features %lld exceed the decode kernel's LDS staging limit", (long long)K);
+  return UQM_OK;
+}
+
+// Routed experts, given device route tables already built in the workspace.
+int run_routed(const uqm_expert_weights* w, const uint16_t* hidden, int64_t T, int64_t k, const Layout& L,
+               void* ws, hipStream_t stream) {
+  using namespace uqm;
+  const int64_t E = w->num_experts, H = w->hidden_size, I = w->intermediate_size;
+  const int grid_y = static_cast<int>(E < T * k ? E : T * k);
+  const int nt = static_cast<int>(T < 4 ? T : 4);
+  GemvArgs g{};
+  g.w[0] = static_cast<const uint8_t*>(w->gate);
+  g.w[1] = static_cast<const uint8_t*>(w->up);
+  g.s[0] = w->gate_scales;
+  g.s[1] = w->up_scales;
+  g.rows = I;
+  g.K = H;
+  g.group = w->group_size;
+  g.x = hidden;
+  g.ldx = H;
+  g.x_div = static_cast<int32_t>(k);
+  g.route_order = at<int32_t>(ws, L.route_order);
+  g.expert_offsets = at<int32_t>(ws, L.expert_offsets);
+  g.active_experts = at<int32_t>(ws, L.active_experts);
+  g.active_count = at<int32_t>(ws, L.counters);
+  g.out = at<uint16_t>(ws, L.h_routed);
+  g.ldo = I;
+  int rc = hip_check(launch_expert_gemv(w->encoding, 2, kModeSilu, g, grid_y, nt, stream), "gate/up launch");
+  if (rc) return rc;
+  GemvArgs d = g;
+  d.w[0] = static_cast<const uint8_t*>(w->down);
+  d.w[1] = nullptr;
+  d.s[0] = w->down_scales;
+  d.s[1] = nullptr;
+  d.rows = H;
+  d.K = I;
+  d.x = at<uint16_t>(ws, L.h_routed);
+  d.ldx = I;
+  d.x_div = 1;
+  d.out = at<float>(ws, L.y_routed);
+  d.ldo = H;
+  return hip_check(launch_expert_gemv(w->encoding, 1, kModeF32, d, grid_y, nt, stream), "down launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int uqm_abi_version(void) { return UQM_ABI_VERSION; }
+
+const char* uqm_last_error(void) { return g_error.c_str(); }
+
+int uqm_device_arch(int device, char* buf, int buf_len) {
+  if (buf == nullptr || buf_len <= 0) return fail(UQM_ERR_ARGUMENT, "buffer is NULL");
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return fail(UQM_ERR_HIP, "hipGetDeviceProperties(%d): %s", device, hipGetErrorString(e));
+  snprintf(buf, static_cast<size_t>(buf_len), "%s", prop.gcnArchName);
+  return UQM_OK;
+}
+
+size_t uqm_moe_workspace_bytes(int64_t tokens, int64_t hidden_size, int64_t intermediate_size,
+                               int64_t shared_intermediate_size, int64_t num_experts, int64_t top_k) {
+  if (tokens < 0 || hidden_size <= 0 || intermediate_size <= 0 || shared_intermediate_size < 0 || num_experts <= 0 ||
+      top_k <= 0)
+    return 0;
+  return layout(tokens, hidden_size, intermediate_size, shared_intermediate_size, num_experts, top_k).total;
+}
+
+static int linear_impl(int enc, const void* input, int64_t rows, const void* w, const float* s, int64_t out_features,
+                       int64_t in_features, int64_t group_size, void* output, void* stream) {
+  using namespace uqm;
+  int rc = check_device();
+  if (rc) return rc;
+  if (rows < 0 || out_features <= 0) return fail(UQM_ERR_ARGUMENT, "rows must be >= 0 and out_features > 0");
+  if ((rc = check_matrix(enc, in_features, group_size, w, s, "linear"))) return rc;
+  if (rows == 0) return UQM_OK;
+  if (input == nullptr || output == nullptr || !aligned16(input)) return fail(UQM_ERR_ARGUMENT, "input must be a 16-byte aligned device pointer and output non-NULL");
+  if ((rc = check_lds(enc, in_features, 4))) return rc;
+  GemvArgs a{};
+  a.w[0] = static_cast<const uint8_t*>(w);
+  a.s[0] = s;
+  a.rows = out_features;
+  a.K = in_features;
+  a.group = group_size;
+  a.x = static_cast<const uint16_t*>(input);
+  a.ldx = in_features;
+  a.x_div = 1;
+  a.n_routes = static_cast<int32_t>(rows);
+  a.out = output;
+  a.ldo = out_features;
+  const int nt = static_cast<int>(rows < 4 ? rows : 4);
+  return hip_check(launch_expert_gemv(enc, 1, kModeBF16, a, 1, nt, static_cast<hipStream_t>(stream)), "linear launch");
+}
+
+int uqm_q4_linear(const void* input, int64_t rows, const void* packed, const float* scales, int64_t out_features,
+                  int64_t in_features, int64_t group_size, void* output, void* stream) {
+  return linear_impl(UQM_Q4, input, rows, packed, scales, out_features, in_features, group_size, output, stream);
+}
+
+int uqm_q8_linear(const void* input, int64_t rows, const void* quantized, const float* scales, int64_t out_features,
+                  int64_t in_features, int64_t group_size, void* output, void* stream) {
+  return linear_impl(UQM_Q8, input, rows, quantized, scales, out_features, in_features, group_size, output, stream);
+}
+
+int uqm_bf16_linear(const void* input, int64_t rows, const void* weight, int64_t out_features, int64_t in_features,
+                    void* output, void* stream) {
+  return linear_impl(UQM_BF16, input, rows, weight, nullptr, out_features, in_features, 0, output, stream);
+}
+
+int uqm_route_permute(const int64_t* expert_indices, int64_t tokens, int64_t top_k, int64_t num_experts,
+                      int64_t* route_order, int64_t* expert_offsets, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  using namespace uqm;
+  int rc = check_device();
+  if (rc) return rc;
+  if (tokens < 0 || top_k <= 0 || num_experts <= 0 || num_experts > 256)
+    return fail(UQM_ERR_ARGUMENT, "tokens >= 0, top_k > 0 and num_experts in [1, 256] are required");
+  if (route_order == nullptr || expert_offsets == nullptr || (tokens > 0 && expert_indices == nullptr))
+    return fail(UQM_ERR_ARGUMENT, "route tensors must be non-NULL");
+  const Layout L = layout(tokens, 8, 8, 0, num_experts, top_k);
+  if (workspace == nullptr || workspace_bytes < L.total)
+    return fail(UQM_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
+  RouteTables rt{at<int32_t>(workspace, L.route_expert), at<int32_t>(workspace, L.route_order),
+                 at<int32_t>(workspace, L.expert_offsets), at<int32_t>(workspace, L.active_experts),
+                 at<int32_t>(workspace, L.counters)};
+  return hip_check(launch_route_permute(nullptr, expert_indices, tokens * top_k, num_experts, rt, route_order,
+                                        expert_offsets, static_cast<hipStream_t>(stream)),
+                   "permute launch");
+}
+
+int uqm_router_topk(const void* hidden, int64_t tokens, int64_t hidden_size, const void* router, int64_t num_experts,
+                    int64_t top_k, int32_t norm_topk_prob, void* logits, void* routing_weights,
+                    int64_t* expert_indices, void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace uqm;
+  int rc = check_device();
+  if (rc) return rc;
+  if (tokens < 0 || num_experts <= 0 || num_experts > 256 || top_k <= 0 || top_k > 64 || top_k > num_experts)
+    return fail(UQM_ERR_ARGUMENT, "need tokens >= 0, 1 <= top_k <= min(64, E), E <= 256");
+  if ((rc = check_matrix(UQM_BF16, hidden_size, 0, router, nullptr, "router"))) return rc;
+  if (tokens == 0) return UQM_OK;
+  if (hidden == nullptr || !aligned16(hidden) || routing_weights == nullptr || expert_indices == nullptr)
+    return fail(UQM_ERR_ARGUMENT, "hidden (16-byte aligned), routing_weights and expert_indices are required");
+  if ((rc = check_lds(UQM_BF16, hidden_size, 4))) return rc;
+  const Layout L = layout(tokens, hidden_size, 8, 0, num_experts, top_k);
+  if (workspace == nullptr || workspace_bytes < L.total)
+    return fail(UQM_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint16_t* lg = logits != nullptr ? static_cast<uint16_t*>(logits) : at<uint16_t>(workspace, L.logits);
+  GemvArgs a{};
+  a.w[0] = static_cast<const uint8_t*>(router);
+  a.rows = num_experts;
+  a.K = hidden_size;
+  a.x = static_cast<const uint16_t*>(hidden);
+  a.ldx = hidden_size;
+  a.x_div = 1;
+  a.n_routes = static_cast<int32_t>(tokens);
+  a.out = lg;
+  a.ldo = num_experts;
+  if ((rc = hip_check(launch_expert_gemv(UQM_BF16, 1, kModeBF16, a, 1, static_cast<int>(tokens < 4 ? tokens : 4), s),
+                      "router launch")))
+    return rc;
+  return hip_check(launch_route_topk(lg, num_experts, tokens, num_experts, top_k, norm_topk_prob,
+                                     static_cast<uint16_t*>(routing_weights), expert_indices, nullptr, nullptr, s),
+                   "top-k launch");
+}
+
+int uqm_moe_forward(const uqm_expert_weights* weights, const void* hidden, int64_t tokens,
+                    const int64_t* expert_indices, const void* routing_weights, int64_t top_k, void* output,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace uqm;
+  int rc = check_device();
+  if (rc) return rc;
+  if ((rc = check_experts(weights))) return rc;
+  if (tokens < 0 || top_k <= 0 || top_k > 64) return fail(UQM_ERR_ARGUMENT, "need tokens >= 0 and 1 <= top_k <= 64");
+  if (tokens == 0) return UQM_OK;
+  if (hidden == nullptr || !aligned16(hidden) || expert_indices == nullptr || routing_weights == nullptr ||
+      output == nullptr || !aligned16(output))
+    return fail(UQM_ERR_ARGUMENT, "hidden/output (16-byte aligned), expert_indices and routing_weights are required");
+  if (weights->hidden_size % 4 != 0) return fail(UQM_ERR_ARGUMENT, "hidden size must be a multiple of 4");
+  if ((rc = check_lds(weights->encoding, weights->hidden_size, 4))) return rc;
+  if ((rc = check_lds(weights->encoding, weights->intermediate_size, 4))) return rc;
+  const Layout L = layout(tokens, weights->hidden_size, weights->intermediate_size, 0, weights->num_experts, top_k);
+  if (workspace == nullptr || workspace_bytes < L.total || !aligned16(workspace))
+    return fail(UQM_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required (or misaligned)",
+                workspace_bytes, L.total);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  RouteTables rt{at<int32_t>(workspace, L.route_expert), at<int32_t>(workspace, L.route_order),
+                 at<int32_t>(workspace, L.expert_offsets), at<int32_t>(workspace, L.active_experts),
+                 at<int32_t>(workspace, L.counters)};
+  if ((rc = hip_check(launch_route_permute(nullptr, expert_indices, tokens * top_k, weights->num_experts, rt, nullptr,
+                                           nullptr, s),
+                      "permute launch")))
+    return rc;
+  if ((rc = run_routed(weights, static_cast<const uint16_t*>(hidden), tokens, top_k, L, workspace, s))) return rc;
+  return hip_check(launch_combine(at<float>(workspace, L.y_routed), static_cast<const uint16_t*>(routing_weights),
+                                  expert_indices, tokens, top_k, weights->num_experts, weights->hidden_size, nullptr,
+                                  nullptr, static_cast<uint16_t*>(output), s),
+                   "combine launch");
+}
+
+int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, void* output, void* logits,
+                  void* routing_weights, int64_t* expert_indices, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  using namespace uqm;
+  int rc = check_device();
+  if (rc) return rc;
+  if (layer == nullptr) return fail(UQM_ERR_ARGUMENT, "layer descriptor is NULL");
+  const uqm_expert_weights* w = &layer->experts;
+  if ((rc = check_experts(w))) return rc;
+  const int64_t E = w->num_experts, H = w->hidden_size, k = layer->top_k;
+  if (tokens < 0 || k <= 0 || k > 64 || k > E) return fail(UQM_ERR_ARGUMENT, "need tokens >= 0 and 1 <= top_k <= min(64, E)");
+  if ((rc = check_matrix(UQM_BF16, H, 0, layer->router, nullptr, "router"))) return rc;
+  const int64_t Is = layer->has_shared ? layer->shared_intermediate_size : 0;
+  if (layer->has_shared) {
+    if (Is <= 0) return fail(UQM_ERR_ARGUMENT, "shared_intermediate_size must be positive");
+    if ((rc = check_matrix(UQM_BF16, H, 0, layer->shared_gate, nullptr, "shared gate"))) return rc;
+    if ((rc = check_matrix(UQM_BF16, H, 0, layer->shared_up, nullptr, "shared up"))) return rc;
+    if ((rc = check_matrix(UQM_BF16, Is, 0, layer->shared_down, nullptr, "shared down"))) return rc;
+    if ((rc = check_matrix(UQM_BF16, H, 0, layer->shared_expert_gate, nullptr, "shared expert gate"))) return rc;
+    if ((rc = check_lds(UQM_BF16, Is, 4))) return rc;
+  }
+  if (tokens == 0) return UQM_OK;
+  if (hidden == nullptr || !aligned16(hidden) || output == nullptr || !aligned16(output))
+    return fail(UQM_ERR_ARGUMENT, "hidden and output must be 16-byte aligned device pointers");
+  if (H % 4 != 0) return fail(UQM_ERR_ARGUMENT, "hidden size must be a multiple of 4");
+  if ((rc = check_lds(w->encoding, H, 4))) return rc;
+  if ((rc = check_lds(w->encoding, w->intermediate_size, 4))) return rc;
+  const Layout L = layout(tokens, H, w->intermediate_size, Is, E, k);
+  if (workspace == nullptr || workspace_bytes < L.total || !aligned16(workspace))
+    return fail(UQM_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required (or misaligned)",
+                workspace_bytes, L.total);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t* x = static_cast<const uint16_t*>(hidden);
+  const int nt = static_cast<int>(tokens < 4 ? tokens : 4);
+  const int64_t rows_router = E + (layer->has_shared ? 1 : 0);
+
+  // 1. router logits (+ shared-gate logit in column E)
+  uint16_t* lg = at<uint16_t>(workspace, L.logits);
+  GemvArgs r{};
+  r.w[0] = static_cast<const uint8_t*>(layer->router);
+  if (layer->has_shared) {
+    r.w_tail = static_cast<const uint8_t*>(layer->shared_expert_gate);
+    r.tail_from = E;
+  }
+  r.rows = rows_router;
+  r.K = H;
+  r.x = x;
+  r.ldx = H;
+  r.x_div = 1;
+  r.n_routes = static_cast<int32_t>(tokens);
+  r.out = lg;
+  r.ldo = rows_router;
+  if ((rc = hip_check(launch_expert_gemv(UQM_BF16, 1, kModeBF16, r, 1, nt, s), "router launch"))) return rc;
+  // 2. top-k + permutation
+  uint16_t* wout = routing_weights != nullptr ? static_cast<uint16_t*>(routing_weights) : at<uint16_t>(workspace, L.weights);
+  int64_t* iout = expert_indices != nullptr ? expert_indices : at<int64_t>(workspace, L.indices);
+  float* sg = layer->has_shared ? at<float>(workspace, L.sg) : nullptr;
+  RouteTables rt{at<int32_t>(workspace, L.route_expert), at<int32_t>(workspace, L.route_order),
+                 at<int32_t>(workspace, L.expert_offsets), at<int32_t>(workspace, L.active_experts),
+                 at<int32_t>(workspace, L.counters)};
+  if ((rc = hip_check(launch_route_topk(lg, rows_router, tokens, E, k, layer->norm_topk_prob, wout, iout,
+                                        rt.route_expert, sg, s),
+                      "top-k launch")))
+    return rc;
+  if (logits != nullptr) {
+    if ((rc = hip_check(hipMemcpy2DAsync(logits, 2 * E, lg, 2 * rows_router, 2 * E, tokens, hipMemcpyDeviceToDevice, s),
+                        "logits copy")))
+      return rc;
+  }
+  if ((rc = hip_check(launch_route_permute(rt.route_expert, nullptr, tokens * k, E, rt, nullptr, nullptr, s),
+                      "permute launch")))
+    return rc;
+  // 3. routed experts
+  if ((rc = run_routed(w, x, tokens, k, L, workspace, s))) return rc;
+  // 4. shared expert
+  if (layer->has_shared) {
+    GemvArgs g{};
+    g.w[0] = static_cast<const uint8_t*>(layer->shared_gate);
+    g.w[1] = static_cast<const uint8_t*>(layer->shared_up);
+    g.rows = Is;
+    g.K = H;
+    g.x = x;
+    g.ldx = H;
+    g.x_div = 1;
+    g.n_routes = static_cast<int32_t>(tokens);
+    g.out = at<uint16_t>(workspace, L.h_shared);
+    g.ldo = Is;
+    if ((rc = hip_check(launch_expert_gemv(UQM_BF16, 2, kModeSilu, g, 1, nt, s), "shared gate/up launch"))) return rc;
+    GemvArgs d{};
+    d.w[0] = static_cast<const uint8_t*>(layer->shared_down);
+    d.rows = H;
+    d.K = Is;
+    d.x = at<uint16_t>(workspace, L.h_shared);
+    d.ldx = Is;
+    d.x_div = 1;
+    d.n_routes = static_cast<int32_t>(tokens);
+    d.out = at<float>(workspace, L.y_shared);
+    d.ldo = H;
+    if ((rc = hip_check(launch_expert_gemv(UQM_BF16, 1, kModeF32, d, 1, nt, s), "shared down launch"))) return rc;
+  }
+  // 5. combine
+  return hip_check(launch_combine(at<float>(workspace, L.y_routed), wout, iout, tokens, k, E, H,
+                                  layer->has_shared ? at<float>(workspace, L.y_shared) : nullptr, sg,
+                                  static_cast<uint16_t*>(output), s),
+                   "combine launch");
+}
+
+int uqm_rmsnorm(const void* input, int64_t rows, int64_t hidden_size, const void* weight, float eps, void* output,
+                void* stream) {
+  using namespace uqm;
+  int rc = check_device();
+  if (rc) return rc;
+  if (rows < 0 || hidden_size <= 0) return fail(UQM_ERR_ARGUMENT, "rows >= 0 and hidden_size > 0 required");
+  if (rows == 0) return UQM_OK;
+  if (input == nullptr || output == nullptr) return fail(UQM_ERR_ARGUMENT, "input and output are required");
+  return hip_check(launch_rmsnorm(static_cast<const uint16_t*>(input), rows, hidden_size,
+                                  static_cast<const uint16_t*>(weight), eps, static_cast<uint16_t*>(output),
+                                  static_cast<hipStream_t>(stream)),
+                   "rmsnorm launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,74 @@
+// Internal (C++) interfaces between the kernel translation units and the
+// extern "C" entry points in uqm_api.hip. Nothing here is exported.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "uqm_device.h"
+
+namespace uqm {
+
+enum GemvMode : int { kModeSilu = 0, kModeF32 = 1, kModeBF16 = 2 };
+
+// One expert-grouped GEMV launch. Matrix m of expert e, row r starts at
+// w[m] + (e * rows + r) * row_bytes; its scale for chunk c is
+// s[m][e * scales_per_expert + (r * K + c * elems) / group]: groups run over
+// each expert's flattened tensor, scales_per_expert = ceil(rows * K / group).
+struct GemvArgs {
+  const uint8_t* w[2];
+  // Optional separate storage for rows >= tail_from of matrix 0 (expert 0
+  // only): lets the router GEMV append the shared-expert gate row.
+  const uint8_t* w_tail;
+  int64_t tail_from;
+  const float* s[2];
+  int64_t rows;   // output rows per expert
+  int64_t K;      // input features
+  int64_t group;  // scale group size in elements (Q4/Q8)
+  int64_t scales_per_expert;
+  const uint16_t* x;  // bf16 activations
+  int64_t ldx;        // elements between activation rows
+  int32_t x_div;      // activation row of route r is r / x_div
+  const int32_t* route_order;     // routes sorted by expert; null = identity
+  const int32_t* expert_offsets;  // [E+1] into route_order; null = one group
+  const int32_t* active_experts;  // compact list of experts with routes; null = blockIdx.y
+  const int32_t* active_count;    // device count of active experts; null = gridDim.y
+  int32_t n_routes;               // route count when expert_offsets is null
+  void* out;                      // output row = route id
+  int64_t ldo;
+};
+
+hipError_t launch_expert_gemv(int enc, int nmat, int mode, const GemvArgs& a, int grid_y, int nt,
+                              hipStream_t stream);
+size_t gemv_lds_bytes(int enc, int64_t K, int nt);
+
+// Route tables produced on the device by the top-k / permutation kernels.
+struct RouteTables {
+  int32_t* route_expert;    // [T*k] expert id per route (route = t*k + slot)
+  int32_t* route_order;     // [T*k] routes stably sorted by expert
+  int32_t* expert_offsets;  // [E+1]
+  int32_t* active_experts;  // [min(E, T*k)]
+  int32_t* active_count;    // [1]
+};
+
+// Top-k over bf16 logits [T, ldl] (columns 0..E-1), softmax in FP32, ties to
+// the lower expert id. Writes bf16 weights / int64 indices [T, k], the route
+// expert table, and (if shared_gate != null) sigmoid of column E.
+hipError_t launch_route_topk(const uint16_t* logits, int64_t ldl, int64_t T, int64_t E, int64_t k, int norm,
+                             uint16_t* weights_out, int64_t* indices_out, int32_t* route_expert,
+                             float* shared_gate, hipStream_t stream);
+// Stable counting sort of the route expert table (invalid ids are dropped).
+// If order64/offsets64 are non-null, int64 copies are written too.
+hipError_t launch_route_permute(const int32_t* route_expert, const int64_t* indices64, int64_t n_routes,
+                                int64_t E, const RouteTables& rt, int64_t* order64, int64_t* offsets64,
+                                hipStream_t stream);
+
+// out[t, o] = bf16( sum_s w[t,s] * y[t*k+s, o] + sg[t] * ys[t, o] )
+hipError_t launch_combine(const float* y, const uint16_t* weights, const int64_t* indices, int64_t T, int64_t k,
+                          int64_t E, int64_t H, const float* ys, const float* sg, uint16_t* out,
+                          hipStream_t stream);
+hipError_t launch_rmsnorm(const uint16_t* x, int64_t rows, int64_t H, const uint16_t* weight, float eps,
+                          uint16_t* out, hipStream_t stream);
+
+}  // namespace uqm

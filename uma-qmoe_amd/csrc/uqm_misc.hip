@@ -1,0 +1,88 @@
+// Weighted scatter-combine and RMSNorm.
+//
+// Combine: the reference accumulates each expert's weighted BF16 output with
+// index_add_ in ascending expert order (src/uma_qmoe/custom_op.py:500-504); its
+// fused GPU decode kernel sums the top-k slots in FP32 and rounds once
+// (src/uma_qmoe/native/packed_q4_kernel.cu:1389-1424). Here every route's
+// projection is kept in FP32 at its route index, so the combine is a gather
+// in slot order with one final rounding; the Qwen shared expert and its
+// sigmoid gate (src/uma_qmoe/qwen_compressed_loader.py:82-85) are folded in.
+//
+// RMSNorm: Transformers' Qwen2MoeRMSNorm (modeling_qwen2_moe.py:65-70),
+// variance in FP32, normalised value cast to BF16, then times the weight.
+#include "uqm_internal.h"
+
+namespace uqm {
+
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, const uint16_t* __restrict__ w,
+                                                      const int64_t* __restrict__ idx, int64_t k, int64_t E,
+                                                      int64_t H, const float* __restrict__ ys,
+                                                      const float* __restrict__ sg, uint16_t* __restrict__ out) {
+  const int64_t t = blockIdx.y;
+  const int64_t o = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (o >= H) return;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t s = 0; s < k; ++s) {
+    const int64_t e = idx[t * k + s];
+    if (e < 0 || e >= E) continue;
+    const float ws = bf16_to_f32(w[t * k + s]);
+    const float4 v = *reinterpret_cast<const float4*>(y + (t * k + s) * H + o);
+    acc.x = fmaf(ws, v.x, acc.x);
+    acc.y = fmaf(ws, v.y, acc.y);
+    acc.z = fmaf(ws, v.z, acc.z);
+    acc.w = fmaf(ws, v.w, acc.w);
+  }
+  if (ys != nullptr) {
+    const float g = sg[t];
+    const float4 v = *reinterpret_cast<const float4*>(ys + t * H + o);
+    acc.x = fmaf(g, v.x, acc.x);
+    acc.y = fmaf(g, v.y, acc.y);
+    acc.z = fmaf(g, v.z, acc.z);
+    acc.w = fmaf(g, v.w, acc.w);
+  }
+  const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(acc.x)) | (static_cast<uint32_t>(f32_to_bf16(acc.y)) << 16);
+  const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(acc.z)) | (static_cast<uint32_t>(f32_to_bf16(acc.w)) << 16);
+  *reinterpret_cast<uint2*>(out + t * H + o) = make_uint2(lo, hi);
+}
+
+hipError_t launch_combine(const float* y, const uint16_t* weights, const int64_t* indices, int64_t T, int64_t k,
+                          int64_t E, int64_t H, const float* ys, const float* sg, uint16_t* out,
+                          hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((H / 4 + 255) / 256), static_cast<unsigned>(T));
+  hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, stream, y, weights, indices, k, E, H, ys, sg, out);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, int64_t H,
+                                                      const uint16_t* __restrict__ weight, float eps,
+                                                      uint16_t* __restrict__ out) {
+  __shared__ float part[4];
+  const uint16_t* xr = x + blockIdx.x * H;
+  uint16_t* orow = out + blockIdx.x * H;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < H; i += blockDim.x) {
+    const float v = bf16_to_f32(xr[i]);
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float total = part[0] + part[1] + part[2] + part[3];
+  const float r = rsqrtf(total / static_cast<float>(H) + eps);
+  for (int64_t i = threadIdx.x; i < H; i += blockDim.x) {
+    const float nv = round_bf16(bf16_to_f32(xr[i]) * r);
+    const float wv = weight != nullptr ? bf16_to_f32(weight[i]) : 1.0f;
+    orow[i] = f32_to_bf16(wv * nv);
+  }
+}
+
+hipError_t launch_rmsnorm(const uint16_t* x, int64_t rows, int64_t H, const uint16_t* weight, float eps,
+                          uint16_t* out, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, x, H, weight, eps,
+                     out);
+  return hipGetLastError();
+}
+
+}  // namespace uqm

@@ -1,0 +1,201 @@
+// Router top-k and token->expert permutation.
+//
+// Top-k replaces torch.topk in Transformers' Qwen2MoeTopKRouter.forward
+// (models/qwen2_moe/modeling_qwen2_moe.py:330-336) with an explicit order:
+// larger logit first, then lower expert id. Softmax is FP32 over the BF16
+// logits; weights are cast to BF16 (optionally renormalised first).
+//
+// The permutation replaces the reference's argsort(stable)/bincount/cumsum
+// (src/uma_qmoe/native_backend.py:530-543) with a single-wave stable counting
+// sort: per 64-route chunk, eight wave ballots give every lane the mask of
+// lanes holding the same expert id, so ranks come from one popcount and no
+// comparison sort is needed.
+#include "uqm_internal.h"
+
+namespace uqm {
+
+__global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restrict__ logits, int64_t ldl,
+                                                         int64_t T, int E, int k, int norm,
+                                                         uint16_t* __restrict__ weights_out,
+                                                         int64_t* __restrict__ indices_out,
+                                                         int32_t* __restrict__ route_expert,
+                                                         float* __restrict__ shared_gate) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (t >= T) return;
+  const uint16_t* row = logits + t * ldl;
+
+  float l[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    l[i] = e < E ? bf16_to_f32(row[e]) : -INFINITY;
+    mx = fmaxf(mx, l[i]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  float se = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (lane + 64 * i < E) se += __expf(l[i] - mx);
+  se = wave_sum(se);
+
+  unsigned used = 0;
+  float my_v = -INFINITY;
+  int my_e = -1;
+  for (int s = 0; s < k; ++s) {
+    float bv = -INFINITY;
+    int be = 0x7FFFFFFF;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E && !(used & (1u << i)) && (l[i] > bv || (l[i] == bv && e < be))) {
+        bv = l[i];
+        be = e;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, kWave);
+      const int oe = __shfl_xor(be, o, kWave);
+      if (ov > bv || (ov == bv && oe < be)) {
+        bv = ov;
+        be = oe;
+      }
+    }
+    if ((be & 63) == lane) used |= 1u << (be >> 6);
+    if (lane == s) {
+      my_v = bv;
+      my_e = be;
+    }
+  }
+  float p = lane < k ? __expf(my_v - mx) / se : 0.f;
+  if (norm) p = p / wave_sum(p);
+  if (lane < k) {
+    weights_out[t * k + lane] = f32_to_bf16(p);
+    indices_out[t * k + lane] = my_e;
+    if (route_expert != nullptr) route_expert[t * k + lane] = my_e;
+  }
+  if (shared_gate != nullptr && lane == 0) shared_gate[t] = round_bf16(sigmoidf_(bf16_to_f32(row[E])));
+}
+
+hipError_t launch_route_topk(const uint16_t* logits, int64_t ldl, int64_t T, int64_t E, int64_t k, int norm,
+                             uint16_t* weights_out, int64_t* indices_out, int32_t* route_expert,
+                             float* shared_gate, hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((T + 3) / 4));
+  hipLaunchKernelGGL(route_topk_kernel, grid, dim3(256), 0, stream, logits, ldl, T, static_cast<int>(E),
+                     static_cast<int>(k), norm, weights_out, indices_out, route_expert, shared_gate);
+  return hipGetLastError();
+}
+
+__device__ __forceinline__ int load_route_id(const int32_t* route_expert, const int64_t* indices64, int64_t r,
+                                             int64_t n, int E, bool& valid) {
+  int64_t id = -1;
+  if (r < n) id = indices64 != nullptr ? indices64[r] : static_cast<int64_t>(route_expert[r]);
+  valid = id >= 0 && id < E;
+  return valid ? static_cast<int>(id) : 0;
+}
+
+// One wavefront; E <= 256.
+__global__ __launch_bounds__(64) void route_permute_kernel(const int32_t* __restrict__ route_expert,
+                                                           const int64_t* __restrict__ indices64, int64_t n,
+                                                           int E, int32_t* __restrict__ route_order,
+                                                           int32_t* __restrict__ expert_offsets,
+                                                           int32_t* __restrict__ active_experts,
+                                                           int32_t* __restrict__ active_count,
+                                                           int64_t* __restrict__ order64,
+                                                           int64_t* __restrict__ offsets64) {
+  __shared__ int cnt[256];
+  __shared__ int run[256];
+  const int lane = threadIdx.x;
+  for (int e = lane; e < 256; e += 64) cnt[e] = 0;
+  __syncthreads();
+
+  for (int64_t base = 0; base < n; base += 64) {
+    bool valid;
+    const int id = load_route_id(route_expert, indices64, base + lane, n, E, valid);
+    if (valid) atomicAdd(&cnt[id], 1);
+  }
+  __syncthreads();
+
+  // Exclusive scan over 4 experts per lane.
+  int c4[4];
+  int local = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    c4[i] = cnt[4 * lane + i];
+    local += c4[i];
+  }
+  int incl = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += v;
+  }
+  int pre = incl - local;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * lane + i;
+    if (e < E) {
+      expert_offsets[e] = pre;
+      if (offsets64 != nullptr) offsets64[e] = pre;
+    }
+    run[e] = pre;
+    pre += c4[i];
+  }
+  const int total = __shfl(incl, 63, kWave);
+  if (lane == 0) {
+    expert_offsets[E] = total;
+    if (offsets64 != nullptr) offsets64[E] = total;
+  }
+  __syncthreads();
+
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t base = 0; base < n; base += 64) {
+    bool valid;
+    const int id = load_route_id(route_expert, indices64, base + lane, n, E, valid);
+    uint64_t eq = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (id >> b) & 1;
+      const uint64_t bal = __ballot(bit);
+      eq &= bit ? bal : ~bal;
+    }
+    const int rank = __popcll(eq & lt);
+    int start = 0;
+    if (valid) start = run[id];
+    __syncthreads();
+    if (valid) {
+      const int pos = start + rank;
+      route_order[pos] = static_cast<int32_t>(base + lane);
+      if (order64 != nullptr) order64[pos] = base + lane;
+      if ((eq & lt) == 0) run[id] = start + __popcll(eq);
+    }
+    __syncthreads();
+  }
+
+  int acc = 0;
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    const bool on = e < E && cnt[e] > 0;
+    const uint64_t m = __ballot(on);
+    if (on) active_experts[acc + __popcll(m & lt)] = e;
+    acc += __popcll(m);
+  }
+  if (lane == 0) *active_count = acc;
+}
+
+hipError_t launch_route_permute(const int32_t* route_expert, const int64_t* indices64, int64_t n_routes,
+                                int64_t E, const RouteTables& rt, int64_t* order64, int64_t* offsets64,
+                                hipStream_t stream) {
+  hipLaunchKernelGGL(route_permute_kernel, dim3(1), dim3(64), 0, stream, route_expert, indices64, n_routes,
+                     static_cast<int>(E), rt.route_order, rt.expert_offsets, rt.active_experts, rt.active_count,
+                     order64, offsets64);
+  return hipGetLastError();
+}
+
+}  // namespace uqm
