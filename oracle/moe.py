@@ -17,6 +17,9 @@ models/qwen2_moe/modeling_qwen2_moe.py):
   qwen_block            src/uma_qmoe/qwen_compressed_loader.py:67-86.
   olmoe_block           src/uma_qmoe/compressed_loader.py:58-67.
   rmsnorm               tf:56-70 (Qwen2MoeRMSNorm, weight ones).
+  route_permutation     src/uma_qmoe/native_backend.py:530-543 (stable argsort,
+                        bincount, cumsum -> route_order, expert_offsets[E+1]);
+                        ids outside [0, E) are dropped instead of raising.
 
 The product never imports this module.
 """
@@ -140,6 +143,26 @@ def olmoe_streaming_reference(hidden_states, expert_indices, routing_weights, la
         hidden_states, expert_indices, routing_weights, layer_index, reader, num_experts=64
     )
     return out.to(hidden_states.dtype)
+
+
+def route_permutation(expert_indices, num_experts: int) -> tuple[list[int], list[int]]:
+    """Stable grouping of the routes t*k+slot by expert id, as a counting sort
+    written out in plain Python (src/uma_qmoe/native_backend.py:530-543 does
+    the same with torch.argsort(stable=True), bincount and cumsum). Routes whose
+    id is outside [0, num_experts) are left out. Returns (route_order,
+    expert_offsets) with len(expert_offsets) == num_experts + 1.
+    """
+    flat = [int(v) for v in torch.as_tensor(expert_indices).reshape(-1).tolist()]
+    buckets: list[list[int]] = [[] for _ in range(num_experts)]
+    for route, e in enumerate(flat):
+        if 0 <= e < num_experts:
+            buckets[e].append(route)
+    order: list[int] = []
+    offsets = [0]
+    for b in buckets:
+        order.extend(b)
+        offsets.append(len(order))
+    return order, offsets
 
 
 def topk_ordered(logits: torch.Tensor, k: int) -> torch.Tensor:

@@ -227,3 +227,23 @@ def test_validation_messages_follow_reference():
         om.qwen_streaming_reference(x, torch.full((1, 4), 60), torch.zeros(1, 4), 0, pack)
     with pytest.raises(RuntimeError, match="layer_index"):
         om.olmoe_streaming_reference(x, torch.zeros(1, 8, dtype=torch.int64), torch.zeros(1, 8), 16, pack)
+
+
+def test_route_permutation_matches_reference_torch_calls():
+    """The counting sort equals the reference's stable argsort + bincount +
+    cumsum (src/uma_qmoe/native_backend.py:530-543) on valid ids, and drops
+    out-of-range ids while keeping the rest stable."""
+    g = torch.Generator().manual_seed(7)
+    for t, k, e in [(1, 4, 60), (5, 8, 64), (64, 4, 60), (33, 2, 256)]:
+        idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(t)])
+        order, offsets = om.route_permutation(idx, e)
+        flat = idx.reshape(-1)
+        assert order == torch.argsort(flat, stable=True).tolist()
+        ref_offsets = torch.cat((torch.zeros(1, dtype=torch.int64), torch.bincount(flat, minlength=e).cumsum(0)))
+        assert offsets == ref_offsets.tolist()
+    # duplicates within a token and across tokens keep route order
+    order, offsets = om.route_permutation(torch.tensor([[2, 2], [1, 2]]), 3)
+    assert order == [2, 0, 1, 3] and offsets == [0, 0, 1, 4]
+    # invalid ids vanish; E+1 offsets still cover [0, E]
+    order, offsets = om.route_permutation(torch.tensor([[3, -1], [70, 3], [0, 5]]), 8)
+    assert order == [4, 0, 3, 5] and offsets == [0, 1, 1, 1, 3, 3, 4, 4, 4]
