@@ -99,18 +99,18 @@ def main() -> int:
     shape = syn.CONFIGS[args.config]
     t = args.tokens
 
-    # R distinct instances so the working set exceeds the MALL.
-    probe = syn.build_experts(shape, device=dev, seed=syn.SEED)
-    dense0 = syn.build_dense(shape, device=dev, seed=syn.SEED)
-    per_layer_total = probe.device_storage_bytes + sum(
-        v.numel() * v.element_size() for v in (dense0.router, dense0.shared_gate, dense0.shared_up,
-                                               dense0.shared_down, dense0.shared_expert_gate) if v is not None)
-    r_inst = max(1, math.ceil(args.rotate_bytes / per_layer_total))
-    layers = [probe] + [syn.build_experts(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
-    denses = [dense0] + [syn.build_dense(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
+    # R distinct layer instances whose per-call reads together exceed the
+    # rotation budget (>= 1 GB), so the 256 MB MALL cannot serve the weights.
     x = syn.hidden_states(shape, t, device=dev)
     ws = ext._workspace(dev, t, shape.hidden, shape.intermediate, shape.shared_intermediate, shape.num_experts,
                         shape.top_k)
+    probe = syn.build_experts(shape, device=dev, seed=syn.SEED)
+    dense0 = syn.build_dense(shape, device=dev, seed=syn.SEED)
+    probe_idx = ext.moe_layer(probe, dense0, x, shape.top_k, workspace=ws)[3]
+    probe_bytes = syn.algorithmic_bytes(probe, dense0, int(torch.unique(probe_idx).numel()))
+    r_inst = max(2, math.ceil(args.rotate_bytes / probe_bytes))
+    layers = [probe] + [syn.build_experts(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
+    denses = [dense0] + [syn.build_dense(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
     outs = [torch.empty((t, shape.hidden), dtype=torch.bfloat16, device=dev) for _ in range(r_inst)]
 
     def run_all():
