@@ -16,8 +16,12 @@
  *     BF16: raw bf16 (src/uma_qmoe/target_pack.py:78-89).
  *     Nothing is ever dequantized to memory.
  *   - Kernels run on `stream` (pass torch's current stream). No entry point
- *     allocates device memory or synchronises; temporaries live in the
- *     caller's `workspace`, sized by uqm_moe_workspace_bytes().
+ *     allocates device memory or synchronises (except uqm_workspace_status);
+ *     temporaries live in the caller's `workspace`, sized by
+ *     uqm_moe_workspace_bytes(). The workspace must be zero-filled before its
+ *     first use: its first 256 bytes hold synchronisation words that the
+ *     single-token fused kernel leaves zero again after every launch. Calls
+ *     that overlap in time must not share a workspace.
  *   - Return 0 on success, nonzero UQM_ERR_* otherwise; the message is in
  *     uqm_last_error() (thread-local). Invalid arguments are rejected before
  *     any launch.
@@ -43,6 +47,13 @@ enum {
 };
 
 enum { UQM_Q4 = 0, UQM_Q8 = 1, UQM_BF16 = 2 };
+
+/* Options for uqm_set_option (process-wide). */
+enum {
+  UQM_OPT_FUSED_DECODE = 1,   /* 1 (default): single-token blocks use the fused persistent kernel */
+  UQM_OPT_FUSED_ROUTED_BLOCKS = 2 /* CUs it gives the routed experts when a shared expert is present
+                                     (0, the default: half of the CUs) */
+};
 
 /* Routed-expert weights of one MoE layer (device pointers). */
 typedef struct uqm_expert_weights {
@@ -141,10 +152,23 @@ int uqm_moe_forward(const uqm_expert_weights* weights, const void* hidden, int64
  * (src/uma_qmoe/qwen_compressed_loader.py:67-86) and QuantizedMoEBlock.forward
  * (src/uma_qmoe/compressed_loader.py:58-67). logits [tokens, E] bf16,
  * routing_weights [tokens, k] bf16 and expert_indices [tokens, k] int64 are
- * optional outputs (NULL to skip). */
+ * optional outputs (NULL to skip). With tokens == 1 and a supported shape
+ * (H = 2048, I/Is giving 1-3 / 11 chunks per lane, top_k <= 8, Q4/Q8/BF16)
+ * the whole block is one persistent launch (see uqm_set_option). */
 int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, void* output, void* logits,
                   void* routing_weights, int64_t* expert_indices, void* workspace, size_t workspace_bytes,
                   void* stream);
+
+/* Sets a process-wide option (UQM_OPT_*). No counterpart in the reference:
+ * it selects between this library's own single-token code paths. */
+int uqm_set_option(int option, int64_t value);
+
+/* Synchronously reads (and clears) the sticky error word that the fused
+ * single-token kernel raises when one of its bounded inter-wave waits expires
+ * (which can only happen when its grid is not fully resident, e.g. while
+ * another persistent kernel holds the device). Returns UQM_OK when clean. No
+ * counterpart in the reference. */
+int uqm_workspace_status(void* workspace, size_t workspace_bytes, void* stream);
 
 /* RMSNorm (Transformers Qwen2MoeRMSNorm, modeling_qwen2_moe.py:65-70): bf16 in/out,
  * FP32 variance; weight bf16 [H] or NULL for ones. Used by the 24-layer stack driver. */

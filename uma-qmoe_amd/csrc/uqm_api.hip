@@ -38,7 +38,7 @@ size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 // Workspace carve-up shared by the size query and the entry points.
 struct Layout {
-  size_t counters, route_expert, route_order, expert_offsets, active_experts, logits, weights, indices, sg,
+  size_t fused_sync, fused_hs, fused_hr, fused_yr, counters, route_expert, route_order, expert_offsets, active_experts, logits, weights, indices, sg,
       h_routed, y_routed, h_shared, y_shared, total;
 };
 
@@ -51,6 +51,10 @@ Layout layout(int64_t T, int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k)
     return at;
   };
   const size_t R = static_cast<size_t>(T * k);
+  L.fused_sync = take(4 * uqm::kSyncWords);
+  L.fused_hs = take(4 * static_cast<size_t>(Is));
+  L.fused_hr = take(4 * static_cast<size_t>(k) * I);
+  L.fused_yr = take(8 * static_cast<size_t>(H));
   L.counters = take(256);
   L.route_expert = take(4 * R);
   L.route_order = take(4 * R);
@@ -72,6 +76,10 @@ template <typename P>
 P* at(void* ws, size_t off) {
   return reinterpret_cast<P*>(static_cast<unsigned char*>(ws) + off);
 }
+
+// Process-wide options (uqm_set_option).
+std::atomic<int64_t> g_opt_fused{1};
+std::atomic<int64_t> g_opt_fused_routed_blocks{0};
 
 // Per-device verdict of the gfx950 check: 0 unknown, 1 gfx950, 2 other.
 std::atomic<int> g_device_ok[64];
@@ -358,6 +366,42 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
   const int nt = static_cast<int>(tokens < 4 ? tokens : 4);
   const int64_t rows_router = E + (layer->has_shared ? 1 : 0);
 
+  // Single token: one persistent launch for the whole block.
+  if (tokens == 1 && g_opt_fused.load(std::memory_order_relaxed) != 0 &&
+      fused_config_id(w->encoding, H, w->intermediate_size, Is, k) >= 0 &&
+      (w->encoding == UQM_BF16 || (H % w->group_size == 0 && w->intermediate_size % w->group_size == 0))) {
+    FusedArgs fa{};
+    fa.x = x;
+    fa.router = static_cast<const uint8_t*>(layer->router);
+    fa.shared_expert_gate = static_cast<const uint8_t*>(layer->shared_expert_gate);
+    fa.sg_w = static_cast<const uint8_t*>(layer->shared_gate);
+    fa.su_w = static_cast<const uint8_t*>(layer->shared_up);
+    fa.sd_w = static_cast<const uint8_t*>(layer->shared_down);
+    fa.eg = static_cast<const uint8_t*>(w->gate);
+    fa.eu = static_cast<const uint8_t*>(w->up);
+    fa.ed = static_cast<const uint8_t*>(w->down);
+    fa.egs = w->gate_scales;
+    fa.eus = w->up_scales;
+    fa.eds = w->down_scales;
+    fa.H = H;
+    fa.I = w->intermediate_size;
+    fa.Is = Is;
+    fa.E = static_cast<int>(E);
+    fa.k = static_cast<int>(k);
+    fa.group = w->encoding == UQM_BF16 ? 1 : w->group_size;
+    fa.norm = layer->norm_topk_prob;
+    fa.sync = at<uint32_t>(workspace, L.fused_sync);
+    fa.hs = at<uint32_t>(workspace, L.fused_hs);
+    fa.hr = at<uint32_t>(workspace, L.fused_hr);
+    fa.yr = at<uint64_t>(workspace, L.fused_yr);
+    fa.out = static_cast<uint16_t*>(output);
+    fa.logits_out = static_cast<uint16_t*>(logits);
+    fa.weights_out = static_cast<uint16_t*>(routing_weights);
+    fa.indices_out = expert_indices;
+    const int64_t nr = g_opt_fused_routed_blocks.load(std::memory_order_relaxed);
+    return hip_check(launch_moe_decode_fused(w->encoding, fa, static_cast<int>(nr), s), "fused block launch");
+  }
+
   // 1. router logits (+ shared-gate logit in column E)
   uint16_t* lg = at<uint16_t>(workspace, L.logits);
   GemvArgs r{};
@@ -427,6 +471,37 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
                                   layer->has_shared ? at<float>(workspace, L.y_shared) : nullptr, sg,
                                   static_cast<uint16_t*>(output), s),
                    "combine launch");
+}
+
+int uqm_set_option(int option, int64_t value) {
+  switch (option) {
+    case UQM_OPT_FUSED_DECODE:
+      g_opt_fused.store(value != 0 ? 1 : 0);
+      return UQM_OK;
+    case UQM_OPT_FUSED_ROUTED_BLOCKS:
+      if (value < 0 || value > 4096) return fail(UQM_ERR_ARGUMENT, "routed workgroups must be in [0, 4096]");
+      g_opt_fused_routed_blocks.store(value);
+      return UQM_OK;
+    default:
+      return fail(UQM_ERR_ARGUMENT, "unknown option %d", option);
+  }
+}
+
+int uqm_workspace_status(void* workspace, size_t workspace_bytes, void* stream) {
+  if (workspace == nullptr || workspace_bytes < 4 * uqm::kSyncWords)
+    return fail(UQM_ERR_WORKSPACE, "workspace is NULL or too small");
+  uint32_t word = 0;
+  uint32_t* dev = static_cast<uint32_t*>(workspace) + uqm::kSyncError;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc;
+  if ((rc = hip_check(hipMemcpyAsync(&word, dev, 4, hipMemcpyDeviceToHost, s), "status read"))) return rc;
+  if ((rc = hip_check(hipStreamSynchronize(s), "status sync"))) return rc;
+  if (word == 0) return UQM_OK;
+  const uint32_t zero = 0;
+  if ((rc = hip_check(hipMemcpyAsync(dev, &zero, 4, hipMemcpyHostToDevice, s), "status clear"))) return rc;
+  if ((rc = hip_check(hipStreamSynchronize(s), "status sync"))) return rc;
+  return fail(UQM_ERR_HIP, "a fused launch on this workspace hit its wait bound (error word %u): its output is invalid",
+              word);
 }
 
 int uqm_rmsnorm(const void* input, int64_t rows, int64_t hidden_size, const void* weight, float eps, void* output,

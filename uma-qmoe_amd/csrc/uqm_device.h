@@ -171,36 +171,91 @@ __device__ __forceinline__ float dot_chunk(const uint4 wv, const XFrag<ENC>& f) 
 }
 
 // ------------------------------------------------------- reductions ----
+// Cross-lane exchanges on the VALU (no LDS round trip): DPP within rows of
+// 16 lanes, the gfx950 permlane swaps across rows. xor_partner<O> returns
+// the value of a partner lane whose index differs from this lane's in bit
+// log2(O) and agrees in every higher bit: lane ^ O for O = 1, 2, 16, 32
+// (quad_perm, permlane16/32_swap), lane ^ 7 for O = 4 (row_half_mirror) and
+// lane ^ 15 for O = 8 (row_mirror). That is all a butterfly reduction needs,
+// and, once a reduction has left one value per group of lanes, it reads the
+// neighbouring group's value.
+template <int O>
+__device__ __forceinline__ float xor_partner(float v) {
+  const int u = __float_as_int(v);
+  if constexpr (O == 1) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+  } else if constexpr (O == 2) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+  } else if constexpr (O == 4) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  } else if constexpr (O == 8) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0x140, 0xF, 0xF, false));  // row_mirror
+  } else if constexpr (O == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);  // r[0]: even rows, r[1]: odd rows
+    return __int_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+  } else {
+    static_assert(O == 32, "O must be a power of two <= 32");
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);  // r[0]: low half, r[1]: high half
+    return __int_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+  }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  v += xor_partner<32>(v);
+  v += xor_partner<16>(v);
+  v += xor_partner<8>(v);
+  v += xor_partner<4>(v);
+  v += xor_partner<2>(v);
+  v += xor_partner<1>(v);
   return v;
 }
 
-// Reduces V = 2^m per-lane values over the wave with V-1+6-m shuffles.
+template <int O>
+__device__ __forceinline__ float wave_max_step(float v) {
+  return fmaxf(v, xor_partner<O>(v));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = wave_max_step<32>(v);
+  v = wave_max_step<16>(v);
+  v = wave_max_step<8>(v);
+  v = wave_max_step<4>(v);
+  v = wave_max_step<2>(v);
+  return wave_max_step<1>(v);
+}
+
+// Halving butterfly stage with partner distance O over n live values.
+template <int O, int N>
+__device__ __forceinline__ void multi_sum_stage(float* buf) {
+  const bool upper = (threadIdx.x & O) != 0;
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const float keep = upper ? buf[i + N / 2] : buf[i];
+    const float send = upper ? buf[i] : buf[i + N / 2];
+    buf[i] = keep + xor_partner<O>(send);
+  }
+}
+
+// Reduces V = 2^m per-lane values over the wave with V-1+6-m exchanges.
 // On return every lane holds the full sum of value index lane >> (6 - m).
 template <int V>
 __device__ __forceinline__ float wave_multi_sum(float (&v)[V]) {
   static_assert((V & (V - 1)) == 0 && V >= 1 && V <= 64, "V must be a power of two <= 64");
-  const int lane = threadIdx.x & (kWave - 1);
   float buf[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) buf[i] = v[i];
-  int n = V;
-  int o = 32;
-#pragma unroll
-  for (; n > 1; n >>= 1, o >>= 1) {
-    const bool upper = (lane & o) != 0;
-#pragma unroll
-    for (int i = 0; i < n / 2; ++i) {
-      const float keep = upper ? buf[i + n / 2] : buf[i];
-      const float send = upper ? buf[i] : buf[i + n / 2];
-      buf[i] = keep + __shfl_xor(send, o, kWave);
-    }
-  }
+  if constexpr (V >= 2) multi_sum_stage<32, V>(buf);
+  if constexpr (V >= 4) multi_sum_stage<16, V / 2>(buf);
+  if constexpr (V >= 8) multi_sum_stage<8, V / 4>(buf);
+  if constexpr (V >= 16) multi_sum_stage<4, V / 8>(buf);
+  if constexpr (V >= 32) multi_sum_stage<2, V / 16>(buf);
+  if constexpr (V >= 64) multi_sum_stage<1, V / 32>(buf);
   float r = buf[0];
-#pragma unroll
-  for (; o > 0; o >>= 1) r += __shfl_xor(r, o, kWave);
+  if constexpr (V < 2) r += xor_partner<32>(r);
+  if constexpr (V < 4) r += xor_partner<16>(r);
+  if constexpr (V < 8) r += xor_partner<8>(r);
+  if constexpr (V < 16) r += xor_partner<4>(r);
+  if constexpr (V < 32) r += xor_partner<2>(r);
+  if constexpr (V < 64) r += xor_partner<1>(r);
   return r;
 }
 

@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void expert_gemv_kernel(GemvArgs a) {
     constexpr int kLog2V = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
     const int j = lane >> (6 - kLog2V);
     float other = 0.f;
-    if constexpr (NMAT == 2) other = __shfl_xor(r, 32, kWave);
+    if constexpr (NMAT == 2) other = xor_partner<32>(r);
     const bool writer = (lane & ((64 >> kLog2V) - 1)) == 0;
     const int t = j % NT;
     const int f = (j / NT) % FPW;

@@ -68,6 +68,45 @@ hipError_t launch_route_permute(const int32_t* route_expert, const int64_t* indi
 hipError_t launch_combine(const float* y, const uint16_t* weights, const int64_t* indices, int64_t T, int64_t k,
                           int64_t E, int64_t H, const float* ys, const float* sg, uint16_t* out,
                           hipStream_t stream);
+// Single-token fused MoE block (uqm_fused.hip). Sync words live in `sync`
+// (zero before the first launch): an epoch that the kernel advances on every
+// launch, a finished-workgroup counter it returns to zero, and a sticky error
+// word it raises when one of its bounded waits expires.
+enum : int { kSyncEpoch = 0, kSyncBlocksDone = 1, kSyncError = 4 };
+constexpr int kSyncWords = 64;
+
+struct FusedArgs {
+  const uint16_t* x;                   // [H] bf16, 16-byte aligned
+  const uint8_t* router;               // [E, H] bf16
+  const uint8_t* shared_expert_gate;   // [H] bf16 (shared expert only)
+  const uint8_t* sg_w;                 // shared gate [Is, H] bf16
+  const uint8_t* su_w;                 // shared up   [Is, H] bf16
+  const uint8_t* sd_w;                 // shared down [H, Is] bf16
+  const uint8_t* eg;                   // routed gate [E, I, H] encoded
+  const uint8_t* eu;                   // routed up   [E, I, H]
+  const uint8_t* ed;                   // routed down [E, H, I]
+  const float* egs;                    // scales (Q4/Q8), group along the row
+  const float* eus;
+  const float* eds;
+  int64_t H, I, Is;
+  int E, k, group, norm;
+  int routed_blocks;                   // set by the launcher
+  uint32_t* sync;                      // kSyncWords words
+  uint32_t* hs;                        // [Is] epoch-tagged shared SiLU products
+  uint32_t* hr;                        // [k, I] epoch-tagged routed SiLU products
+  uint64_t* yr;                        // [H] epoch-tagged routed outputs (fp32)
+  uint16_t* out;                       // [H]
+  uint16_t* logits_out;                // optional [E]
+  uint16_t* weights_out;               // optional [k]
+  int64_t* indices_out;                // optional [k]
+};
+
+// Returns >= 0 when a compiled instantiation covers (encoding, H, I, Is, k).
+int fused_config_id(int enc, int64_t H, int64_t I, int64_t Is, int64_t k);
+// routed_blocks: CUs given to the routed experts when a shared expert is
+// present (0 = half of the CUs).
+hipError_t launch_moe_decode_fused(int enc, const FusedArgs& a, int routed_blocks, hipStream_t stream);
+
 hipError_t launch_rmsnorm(const uint16_t* x, int64_t rows, int64_t H, const uint16_t* weight, float eps,
                           uint16_t* out, hipStream_t stream);
 

@@ -19,6 +19,9 @@ UQM_Q4 = 0
 UQM_Q8 = 1
 UQM_BF16 = 2
 
+UQM_OPT_FUSED_DECODE = 1
+UQM_OPT_FUSED_ROUTED_BLOCKS = 2
+
 ENCODING_IDS = {"q4_group128": UQM_Q4, "q8_group128": UQM_Q8, "bf16_le": UQM_BF16}
 
 ERROR_NAMES = {1: "argument", 2: "hip", 3: "device", 4: "workspace"}
@@ -89,6 +92,8 @@ SIGNATURES = {
         (ctypes.POINTER(LayerWeights), _vp, _i64, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp),
     ),
     "uqm_rmsnorm": (ctypes.c_int, (_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _vp)),
+    "uqm_set_option": (ctypes.c_int, (ctypes.c_int, _i64)),
+    "uqm_workspace_status": (ctypes.c_int, (_vp, ctypes.c_size_t, _vp)),
 }
 
 

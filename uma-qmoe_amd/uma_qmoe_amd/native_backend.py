@@ -149,7 +149,8 @@ class HipExtension:
         n = self.lib.uqm_moe_workspace_bytes(tokens, hidden, inter, shared_inter, experts, top_k)
         if n == 0:
             raise RuntimeError("invalid workspace shape")
-        return self.torch.empty(n, dtype=self.torch.uint8, device=device)
+        # zero-filled: the fused single-token kernel keeps its sync words here
+        return self.torch.zeros(n, dtype=self.torch.uint8, device=device)
 
     def _check_hidden(self, hidden):
         torch = self.torch
@@ -274,6 +275,15 @@ class HipExtension:
             _ptr(dense.shared_down),
             _ptr(dense.shared_expert_gate),
         )
+
+    def set_option(self, option: int, value: int) -> None:
+        _native.check(self.lib.uqm_set_option(int(option), int(value)), "uqm_set_option")
+
+    def workspace_status(self, workspace) -> None:
+        """Raises if a fused launch on ``workspace`` hit its wait bound."""
+        torch = self.torch
+        rc = self.lib.uqm_workspace_status(_ptr(workspace), workspace.numel(), _stream_handle(torch, workspace.device))
+        _native.check(rc, "uqm_workspace_status")
 
     def rmsnorm(self, hidden, eps=1e-6, weight=None):
         torch = self.torch
