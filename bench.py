@@ -42,6 +42,11 @@ def parse_args():
     ap.add_argument("--rotate-bytes", type=float, default=1.1e9)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-batch32", dest="batch32", action="store_false",
+                    help="skip the batch-32 decode measurement reported beside the batch-1 value")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run 8 device-to-device copies of BYTES bytes (calibrates rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE against a kernel of known traffic) and exit")
     return ap.parse_args()
 
 
@@ -84,34 +89,49 @@ def cpu_baseline(shape, seconds: float):
     }
 
 
-def main() -> int:
-    args = parse_args()
-    if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
-        return 2
-    import torch
+BASELINE_METRIC = "MoE layer \u00b5s/token + achieved HBM GB/s (% peak), Qwen-MoE shape, batch 1 & 32"
 
-    from uma_qmoe_amd import synthetic as syn
-    from uma_qmoe_amd.native_backend import load_native_extension
 
-    _platform, ext = load_native_extension()
+def profiled_traffic(workload: str):
+    """HBM bytes per launch of the fused kernel from the committed rocprofv3
+    summary (profiles/moe_decode_fused_c2.md), only while the kernel sources
+    still hash to the digest recorded with the measurement."""
+    import re
+
+    from uma_qmoe_amd.native_backend import native_kernel_source_sha256
+
+    path = ROOT / "profiles" / "moe_decode_fused_c2.md"
+    if not path.is_file():
+        return None
+    m = re.search(r"```json\n(.*?)\n```", path.read_text(), re.S)
+    if m is None:
+        return None
+    data = json.loads(m.group(1))
+    if data.get("workload") != workload or data.get("source_sha256") != native_kernel_source_sha256():
+        return None
+    return int(data["traffic_bytes_per_launch"])
+
+
+def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
+    """Times one MoE block call on `tokens` tokens: R distinct layer instances
+    whose per-call reads together exceed `rotate_bytes` (>= 1 GB, so the 256 MB
+    MALL cannot serve the weights) are captured in one HIP graph, and the
+    graph is replayed between HIP events on torch's current stream (the
+    stream the kernels run on). Returns us per layer call and algorithmic
+    GB/s (each distinct selected expert counted once, plus router and shared
+    expert)."""
     dev = torch.device("cuda:0")
-    shape = syn.CONFIGS[args.config]
-    t = args.tokens
-
-    # R distinct layer instances whose per-call reads together exceed the
-    # rotation budget (>= 1 GB), so the 256 MB MALL cannot serve the weights.
-    x = syn.hidden_states(shape, t, device=dev)
-    ws = ext._workspace(dev, t, shape.hidden, shape.intermediate, shape.shared_intermediate, shape.num_experts,
+    x = syn.hidden_states(shape, tokens, device=dev)
+    ws = ext._workspace(dev, tokens, shape.hidden, shape.intermediate, shape.shared_intermediate, shape.num_experts,
                         shape.top_k)
     probe = syn.build_experts(shape, device=dev, seed=syn.SEED)
     dense0 = syn.build_dense(shape, device=dev, seed=syn.SEED)
     probe_idx = ext.moe_layer(probe, dense0, x, shape.top_k, workspace=ws)[3]
     probe_bytes = syn.algorithmic_bytes(probe, dense0, int(torch.unique(probe_idx).numel()))
-    r_inst = max(2, math.ceil(args.rotate_bytes / probe_bytes))
+    r_inst = max(2, math.ceil(rotate_bytes / probe_bytes))
     layers = [probe] + [syn.build_experts(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
     denses = [dense0] + [syn.build_dense(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
-    outs = [torch.empty((t, shape.hidden), dtype=torch.bfloat16, device=dev) for _ in range(r_inst)]
+    outs = [torch.empty((tokens, shape.hidden), dtype=torch.bfloat16, device=dev) for _ in range(r_inst)]
 
     def run_all():
         res = []
@@ -130,8 +150,8 @@ def main() -> int:
         run_all()
     torch.cuda.synchronize()
 
-    replays = max(1, math.ceil(args.steps / r_inst))
-    warm = max(1, math.ceil(args.warmup / r_inst))
+    replays = max(1, math.ceil(steps / r_inst))
+    warm = max(1, math.ceil(warmup / r_inst))
     for _ in range(warm):
         graph.replay()
     torch.cuda.synchronize()
@@ -146,18 +166,46 @@ def main() -> int:
         torch.cuda.synchronize()
         samples.append(start.elapsed_time(stop))
     ms_total = sorted(samples)[1]
-    steps = replays * r_inst
-    us_per_layer = ms_total * 1000.0 / steps
+    n = replays * r_inst
+    us = ms_total * 1000.0 / n
     mean_bytes = sum(algo_bytes) / len(algo_bytes)
-    achieved = mean_bytes / (us_per_layer * 1e-6) / 1e9
+    del graph, layers, denses, outs, ws
+    torch.cuda.empty_cache()
+    return {"us_per_layer": us, "gbps": mean_bytes / (us * 1e-6) / 1e9, "bytes": mean_bytes, "instances": r_inst,
+            "steps": n, "warmup": warm * r_inst}
 
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        return 2
+    import torch
+
+    if args.copy_probe:
+        src = torch.empty(args.copy_probe, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": args.copy_probe, "copies": 8}), flush=True)
+        return 0
+
+    from uma_qmoe_amd import synthetic as syn
+    from uma_qmoe_amd.native_backend import load_native_extension
+
+    _platform, ext = load_native_extension()
+    shape = syn.CONFIGS[args.config]
+    head = measure(torch, syn, ext, shape, args.tokens, args.steps, args.warmup, args.rotate_bytes)
+    us_per_layer = head["us_per_layer"]
+    achieved = head["gbps"]
     line = {
-        "metric": "MoE layer us/token (Qwen1.5-MoE W4A16 block, decode batch 1) + achieved HBM GB/s",
+        "metric": BASELINE_METRIC,
         "value": round(us_per_layer, 3),
         "unit": "us/token",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": warm * r_inst,
+        "steps": head["steps"],
+        "warmup": head["warmup"],
         "ms_per_step": round(us_per_layer / 1000.0, 6),
         "higher_is_better": False,
         "scaling": "weak",
@@ -167,21 +215,31 @@ def main() -> int:
         "config": {
             "workload": f"{shape.name}: one MoE block (router + top-{shape.top_k} of {shape.num_experts} Q4 experts "
                         f"I={shape.intermediate} + bf16 shared expert {shape.shared_intermediate}), H={shape.hidden}",
-            "tokens": t,
-            "rotated_instances": r_inst,
+            "tokens": args.tokens,
+            "rotated_instances": head["instances"],
             "parallelism": "single GPU",
         },
-        "tokens_per_s": round(t / (us_per_layer * 1e-6), 1),
-        "algorithmic_bytes_per_call": int(mean_bytes),
+        "tokens_per_s": round(args.tokens / (us_per_layer * 1e-6), 1),
+        "algorithmic_bytes_per_call": int(head["bytes"]),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(shape.name) if args.tokens == 1 else None,
         },
     }
+    if args.batch32 and args.tokens == 1:
+        b32 = measure(torch, syn, ext, shape, 32, max(32, args.steps // 4), max(8, args.warmup // 4), args.rotate_bytes)
+        line["batch32"] = {
+            "us_per_layer": round(b32["us_per_layer"], 3),
+            "us_per_token": round(b32["us_per_layer"] / 32, 3),
+            "tokens_per_s": round(32 / (b32["us_per_layer"] * 1e-6), 1),
+            "algorithmic_bytes_per_call": int(b32["bytes"]),
+            "achieved_gbps": round(b32["gbps"], 1),
+            "frac": round(b32["gbps"] / HBM_PEAK_GBPS, 4),
+        }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(shape, args.cpu_seconds)
     print(json.dumps(line), flush=True)
