@@ -51,8 +51,10 @@ enum { UQM_Q4 = 0, UQM_Q8 = 1, UQM_BF16 = 2 };
 /* Options for uqm_set_option (process-wide). */
 enum {
   UQM_OPT_FUSED_DECODE = 1,   /* 1 (default): single-token blocks use the fused persistent kernel */
-  UQM_OPT_FUSED_ROUTED_BLOCKS = 2 /* CUs it gives the routed experts when a shared expert is present
-                                     (0, the default: half of the CUs) */
+  UQM_OPT_FUSED_ROUTED_BLOCKS = 2, /* CUs it gives the routed experts when a shared expert is present
+                                      (0, the default: half of the CUs) */
+  UQM_OPT_MFMA_MIN_TOKENS = 3      /* token count from which multi-token calls run the expert projections
+                                      as MFMA grouped GEMMs (default 2; 0 = never, batched GEMV instead) */
 };
 
 /* Routed-expert weights of one MoE layer (device pointers). */

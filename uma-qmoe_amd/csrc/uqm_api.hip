@@ -37,9 +37,12 @@ int elems_per_chunk(int enc) { return enc == UQM_Q4 ? 32 : enc == UQM_Q8 ? 16 : 
 size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 // Workspace carve-up shared by the size query and the entry points.
+// FP32 partial outputs a K-split MFMA down projection may write.
+constexpr int kMaxSplit = 4;
+
 struct Layout {
-  size_t fused_sync, fused_hs, fused_hr, fused_yr, counters, route_expert, route_order, expert_offsets, active_experts, logits, weights, indices, sg,
-      h_routed, y_routed, h_shared, y_shared, total;
+  size_t fused_sync, fused_hs, fused_hr, fused_yr, counters, route_expert, route_order, expert_offsets, active_experts,
+      tiles, logits, weights, indices, sg, h_routed, y_routed, h_shared, y_shared, total;
 };
 
 Layout layout(int64_t T, int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k) {
@@ -60,14 +63,15 @@ Layout layout(int64_t T, int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k)
   L.route_order = take(4 * R);
   L.expert_offsets = take(4 * (E + 1));
   L.active_experts = take(4 * E);
+  L.tiles = take(8 * (E + R));
   L.logits = take(2 * static_cast<size_t>(T) * (E + 1));
   L.weights = take(2 * R);
   L.indices = take(8 * R);
   L.sg = take(4 * static_cast<size_t>(T));
   L.h_routed = take(2 * R * I);
-  L.y_routed = take(4 * R * H);
+  L.y_routed = take(4 * R * H * (T > 1 ? kMaxSplit : 1));
   L.h_shared = take(2 * static_cast<size_t>(T) * Is);
-  L.y_shared = take(4 * static_cast<size_t>(T) * H);
+  L.y_shared = take(4 * static_cast<size_t>(T) * H * (T > 1 && Is > 0 ? kMaxSplit : 1));
   L.total = off;
   return L;
 }
@@ -80,6 +84,79 @@ P* at(void* ws, size_t off) {
 // Process-wide options (uqm_set_option).
 std::atomic<int64_t> g_opt_fused{1};
 std::atomic<int64_t> g_opt_fused_routed_blocks{0};
+std::atomic<int64_t> g_opt_mfma_min_tokens{2};
+
+// Compute units of the current device (cached per device id).
+std::atomic<int> g_cus[64];
+
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < 64) {
+    const int v = g_cus[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev >= 0 && dev < 64) g_cus[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// Launch shape of one MFMA grouped GEMM (see launch_expert_mfma).
+struct MfmaPlan {
+  int nb = 1, kw = 1, rt = 1, ksplit = 1;
+};
+
+// 16-route tiles per workgroup from the mean routes per expert.
+int nb_for(int enc, double mean_routes) {
+  if (mean_routes <= 16) return 1;
+  if (mean_routes <= 32) return 2;
+  if (mean_routes <= 64 || enc != UQM_BF16) return 4;
+  return 8;
+}
+
+// Enough workgroups to cover the chip: more rows per wave when there is
+// plenty of work, waves (then workgroups) along K when there is little.
+MfmaPlan plan_mfma(int nmat, int64_t rows, int64_t K, int nb, int64_t tiles, int cus, int max_split) {
+  MfmaPlan p;
+  p.nb = nb;
+  if (nmat == 2) {
+    if (nb <= 2 && rows / 64 * tiles < cus) p.kw = 4;
+    return p;
+  }
+  if (rows % 128 == 0 && rows / 128 * tiles >= 2 * cus) {
+    p.rt = 2;
+    return p;
+  }
+  if (rows / 64 * tiles >= cus) return p;
+  if (nb <= 2) p.kw = 4;
+  const int64_t wgs = rows / (p.kw == 4 ? 16 : 64) * tiles;
+  int64_t ks = (cus + wgs - 1) / wgs;
+  const int64_t max_by_k = (K / 128) / (2 * p.kw);  // keep >= 2 steps per wave
+  if (ks > max_split) ks = max_split;
+  if (ks > max_by_k) ks = max_by_k;
+  p.ksplit = ks < 1 ? 1 : static_cast<int>(ks);
+  return p;
+}
+
+bool routed_uses_mfma(const uqm_expert_weights* w, int64_t T) {
+  const int64_t min_t = g_opt_mfma_min_tokens.load(std::memory_order_relaxed);
+  return min_t > 0 && T >= min_t && uqm::mfma_supported(w->encoding, w->intermediate_size, w->hidden_size, w->group_size) &&
+         uqm::mfma_supported(w->encoding, w->hidden_size, w->intermediate_size, w->group_size);
+}
+
+bool shared_uses_mfma(int64_t H, int64_t Is, int64_t T) {
+  const int64_t min_t = g_opt_mfma_min_tokens.load(std::memory_order_relaxed);
+  return min_t > 0 && T >= min_t && uqm::mfma_supported(UQM_BF16, Is, H, 0) && uqm::mfma_supported(UQM_BF16, H, Is, 0);
+}
+
+// Route tile size the routed MFMA path uses (0 = GEMV path).
+int routed_tile_tokens(const uqm_expert_weights* w, int64_t T, int64_t k) {
+  if (!routed_uses_mfma(w, T)) return 0;
+  const int64_t R = T * k;
+  const int64_t active = R < w->num_experts ? R : w->num_experts;
+  return 16 * nb_for(w->encoding, static_cast<double>(R) / static_cast<double>(active));
+}
 
 // Per-device verdict of the gfx950 check: 0 unknown, 1 gfx950, 2 other.
 std::atomic<int> g_device_ok[64];
@@ -132,12 +209,60 @@ int check_lds(int enc, int64_t K, int nt) {
   return UQM_OK;
 }
 
-// Routed experts, given device route tables already built in the workspace.
+// Routed experts, given device route tables already built in the workspace
+// (with route tiles of `tile_tokens` when the MFMA path is used). Returns the
+// number of FP32 partials written to y_routed through *parts.
 int run_routed(const uqm_expert_weights* w, const uint16_t* hidden, int64_t T, int64_t k, const Layout& L,
-               void* ws, hipStream_t stream) {
+               void* ws, int tile_tokens, int* parts, hipStream_t stream) {
   using namespace uqm;
   const int64_t E = w->num_experts, H = w->hidden_size, I = w->intermediate_size;
-  const int grid_y = static_cast<int>(E < T * k ? E : T * k);
+  const int64_t R = T * k;
+  *parts = 1;
+  if (tile_tokens > 0) {
+    const int nb = tile_tokens / 16;
+    const int64_t active = R < E ? R : E;
+    const int cus = device_cus();
+    MfmaArgs g{};
+    g.w[0] = static_cast<const uint8_t*>(w->gate);
+    g.w[1] = static_cast<const uint8_t*>(w->up);
+    g.s[0] = w->gate_scales;
+    g.s[1] = w->up_scales;
+    g.rows = I;
+    g.K = H;
+    g.group = w->group_size;
+    g.x = hidden;
+    g.ldx = H;
+    g.x_div = static_cast<int32_t>(k);
+    g.route_order = at<int32_t>(ws, L.route_order);
+    g.expert_offsets = at<int32_t>(ws, L.expert_offsets);
+    g.tiles = at<int32_t>(ws, L.tiles);
+    g.tile_count = at<int32_t>(ws, L.counters) + 1;
+    g.tile_bound = static_cast<int32_t>(active + R / tile_tokens);
+    g.out = at<uint16_t>(ws, L.h_routed);
+    g.ldo = I;
+    g.ksplit = 1;
+    const MfmaPlan pg = plan_mfma(2, I, H, nb, active, cus, 1);
+    int rc = hip_check(launch_expert_mfma(w->encoding, 2, g, pg.nb, pg.kw, pg.rt, stream), "gate/up MFMA launch");
+    if (rc) return rc;
+    MfmaArgs d = g;
+    d.w[0] = static_cast<const uint8_t*>(w->down);
+    d.w[1] = nullptr;
+    d.s[0] = w->down_scales;
+    d.s[1] = nullptr;
+    d.rows = H;
+    d.K = I;
+    d.x = at<uint16_t>(ws, L.h_routed);
+    d.ldx = I;
+    d.x_div = 1;
+    d.out = at<float>(ws, L.y_routed);
+    d.ldo = H;
+    d.part_stride = R * H;
+    const MfmaPlan pd = plan_mfma(1, H, I, nb, active, cus, T > 1 ? kMaxSplit : 1);
+    d.ksplit = pd.ksplit;
+    *parts = pd.ksplit;
+    return hip_check(launch_expert_mfma(w->encoding, 1, d, pd.nb, pd.kw, pd.rt, stream), "down MFMA launch");
+  }
+  const int grid_y = static_cast<int>(E < R ? E : R);
   const int nt = static_cast<int>(T < 4 ? T : 4);
   GemvArgs g{};
   g.w[0] = static_cast<const uint8_t*>(w->gate);
@@ -171,6 +296,76 @@ int run_routed(const uqm_expert_weights* w, const uint16_t* hidden, int64_t T, i
   d.out = at<float>(ws, L.y_routed);
   d.ldo = H;
   return hip_check(launch_expert_gemv(w->encoding, 1, kModeF32, d, grid_y, nt, stream), "down launch");
+}
+
+// Shared expert on T tokens: h_shared = silu(x Wg^T) * (x Wu^T), y_shared =
+// h_shared Wd^T (FP32, *parts K-split partials).
+int run_shared(const uqm_layer_weights* layer, const uint16_t* x, int64_t T, int64_t H, const Layout& L, void* ws,
+               int* parts, hipStream_t stream) {
+  using namespace uqm;
+  const int64_t Is = layer->shared_intermediate_size;
+  *parts = 1;
+  if (shared_uses_mfma(H, Is, T)) {
+    const int nb = nb_for(UQM_BF16, static_cast<double>(T));
+    const int ntok = 16 * nb;
+    const int64_t tiles = (T + ntok - 1) / ntok;
+    const int cus = device_cus();
+    MfmaArgs g{};
+    g.w[0] = static_cast<const uint8_t*>(layer->shared_gate);
+    g.w[1] = static_cast<const uint8_t*>(layer->shared_up);
+    g.rows = Is;
+    g.K = H;
+    g.x = x;
+    g.ldx = H;
+    g.x_div = 1;
+    g.tile_bound = static_cast<int32_t>(tiles);
+    g.n_routes = static_cast<int32_t>(T);
+    g.out = at<uint16_t>(ws, L.h_shared);
+    g.ldo = Is;
+    g.ksplit = 1;
+    const MfmaPlan pg = plan_mfma(2, Is, H, nb, tiles, cus, 1);
+    int rc = hip_check(launch_expert_mfma(UQM_BF16, 2, g, pg.nb, pg.kw, pg.rt, stream), "shared gate/up MFMA launch");
+    if (rc) return rc;
+    MfmaArgs d = g;
+    d.w[0] = static_cast<const uint8_t*>(layer->shared_down);
+    d.w[1] = nullptr;
+    d.rows = H;
+    d.K = Is;
+    d.x = at<uint16_t>(ws, L.h_shared);
+    d.ldx = Is;
+    d.out = at<float>(ws, L.y_shared);
+    d.ldo = H;
+    d.part_stride = T * H;
+    const MfmaPlan pd = plan_mfma(1, H, Is, nb, tiles, cus, T > 1 ? kMaxSplit : 1);
+    d.ksplit = pd.ksplit;
+    *parts = pd.ksplit;
+    return hip_check(launch_expert_mfma(UQM_BF16, 1, d, pd.nb, pd.kw, pd.rt, stream), "shared down MFMA launch");
+  }
+  const int nt = static_cast<int>(T < 4 ? T : 4);
+  GemvArgs g{};
+  g.w[0] = static_cast<const uint8_t*>(layer->shared_gate);
+  g.w[1] = static_cast<const uint8_t*>(layer->shared_up);
+  g.rows = Is;
+  g.K = H;
+  g.x = x;
+  g.ldx = H;
+  g.x_div = 1;
+  g.n_routes = static_cast<int32_t>(T);
+  g.out = at<uint16_t>(ws, L.h_shared);
+  g.ldo = Is;
+  int rc = hip_check(launch_expert_gemv(UQM_BF16, 2, kModeSilu, g, 1, nt, stream), "shared gate/up launch");
+  if (rc) return rc;
+  GemvArgs d{};
+  d.w[0] = static_cast<const uint8_t*>(layer->shared_down);
+  d.rows = H;
+  d.K = Is;
+  d.x = at<uint16_t>(ws, L.h_shared);
+  d.ldx = Is;
+  d.x_div = 1;
+  d.n_routes = static_cast<int32_t>(T);
+  d.out = at<float>(ws, L.y_shared);
+  d.ldo = H;
+  return hip_check(launch_expert_gemv(UQM_BF16, 1, kModeF32, d, 1, nt, stream), "shared down launch");
 }
 
 }  // namespace
@@ -254,9 +449,10 @@ int uqm_route_permute(const int64_t* expert_indices, int64_t tokens, int64_t top
     return fail(UQM_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
   RouteTables rt{at<int32_t>(workspace, L.route_expert), at<int32_t>(workspace, L.route_order),
                  at<int32_t>(workspace, L.expert_offsets), at<int32_t>(workspace, L.active_experts),
-                 at<int32_t>(workspace, L.counters)};
+                 at<int32_t>(workspace, L.counters), at<int32_t>(workspace, L.tiles),
+                 at<int32_t>(workspace, L.counters) + 1};
   return hip_check(launch_route_permute(nullptr, expert_indices, tokens * top_k, num_experts, rt, route_order,
-                                        expert_offsets, static_cast<hipStream_t>(stream)),
+                                        expert_offsets, 0, static_cast<hipStream_t>(stream)),
                    "permute launch");
 }
 
@@ -318,15 +514,21 @@ int uqm_moe_forward(const uqm_expert_weights* weights, const void* hidden, int64
   hipStream_t s = static_cast<hipStream_t>(stream);
   RouteTables rt{at<int32_t>(workspace, L.route_expert), at<int32_t>(workspace, L.route_order),
                  at<int32_t>(workspace, L.expert_offsets), at<int32_t>(workspace, L.active_experts),
-                 at<int32_t>(workspace, L.counters)};
+                 at<int32_t>(workspace, L.counters), at<int32_t>(workspace, L.tiles),
+                 at<int32_t>(workspace, L.counters) + 1};
+  const int tile_tokens = routed_tile_tokens(weights, tokens, top_k);
   if ((rc = hip_check(launch_route_permute(nullptr, expert_indices, tokens * top_k, weights->num_experts, rt, nullptr,
-                                           nullptr, s),
+                                           nullptr, tile_tokens, s),
                       "permute launch")))
     return rc;
-  if ((rc = run_routed(weights, static_cast<const uint16_t*>(hidden), tokens, top_k, L, workspace, s))) return rc;
-  return hip_check(launch_combine(at<float>(workspace, L.y_routed), static_cast<const uint16_t*>(routing_weights),
-                                  expert_indices, tokens, top_k, weights->num_experts, weights->hidden_size, nullptr,
-                                  nullptr, static_cast<uint16_t*>(output), s),
+  int parts = 1;
+  if ((rc = run_routed(weights, static_cast<const uint16_t*>(hidden), tokens, top_k, L, workspace, tile_tokens, &parts,
+                       s)))
+    return rc;
+  return hip_check(launch_combine(at<float>(workspace, L.y_routed), parts, tokens * top_k * weights->hidden_size,
+                                  static_cast<const uint16_t*>(routing_weights), expert_indices, tokens, top_k,
+                                  weights->num_experts, weights->hidden_size, nullptr, 1, 0, nullptr,
+                                  static_cast<uint16_t*>(output), s),
                    "combine launch");
 }
 
@@ -425,7 +627,8 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
   float* sg = layer->has_shared ? at<float>(workspace, L.sg) : nullptr;
   RouteTables rt{at<int32_t>(workspace, L.route_expert), at<int32_t>(workspace, L.route_order),
                  at<int32_t>(workspace, L.expert_offsets), at<int32_t>(workspace, L.active_experts),
-                 at<int32_t>(workspace, L.counters)};
+                 at<int32_t>(workspace, L.counters), at<int32_t>(workspace, L.tiles),
+                 at<int32_t>(workspace, L.counters) + 1};
   if ((rc = hip_check(launch_route_topk(lg, rows_router, tokens, E, k, layer->norm_topk_prob, wout, iout,
                                         rt.route_expert, sg, s),
                       "top-k launch")))
@@ -435,41 +638,19 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
                         "logits copy")))
       return rc;
   }
-  if ((rc = hip_check(launch_route_permute(rt.route_expert, nullptr, tokens * k, E, rt, nullptr, nullptr, s),
+  const int tile_tokens = routed_tile_tokens(w, tokens, k);
+  if ((rc = hip_check(launch_route_permute(rt.route_expert, nullptr, tokens * k, E, rt, nullptr, nullptr, tile_tokens, s),
                       "permute launch")))
     return rc;
   // 3. routed experts
-  if ((rc = run_routed(w, x, tokens, k, L, workspace, s))) return rc;
+  int yr_parts = 1, ys_parts = 1;
+  if ((rc = run_routed(w, x, tokens, k, L, workspace, tile_tokens, &yr_parts, s))) return rc;
   // 4. shared expert
-  if (layer->has_shared) {
-    GemvArgs g{};
-    g.w[0] = static_cast<const uint8_t*>(layer->shared_gate);
-    g.w[1] = static_cast<const uint8_t*>(layer->shared_up);
-    g.rows = Is;
-    g.K = H;
-    g.x = x;
-    g.ldx = H;
-    g.x_div = 1;
-    g.n_routes = static_cast<int32_t>(tokens);
-    g.out = at<uint16_t>(workspace, L.h_shared);
-    g.ldo = Is;
-    if ((rc = hip_check(launch_expert_gemv(UQM_BF16, 2, kModeSilu, g, 1, nt, s), "shared gate/up launch"))) return rc;
-    GemvArgs d{};
-    d.w[0] = static_cast<const uint8_t*>(layer->shared_down);
-    d.rows = H;
-    d.K = Is;
-    d.x = at<uint16_t>(workspace, L.h_shared);
-    d.ldx = Is;
-    d.x_div = 1;
-    d.n_routes = static_cast<int32_t>(tokens);
-    d.out = at<float>(workspace, L.y_shared);
-    d.ldo = H;
-    if ((rc = hip_check(launch_expert_gemv(UQM_BF16, 1, kModeF32, d, 1, nt, s), "shared down launch"))) return rc;
-  }
+  if (layer->has_shared && (rc = run_shared(layer, x, tokens, H, L, workspace, &ys_parts, s))) return rc;
   // 5. combine
-  return hip_check(launch_combine(at<float>(workspace, L.y_routed), wout, iout, tokens, k, E, H,
-                                  layer->has_shared ? at<float>(workspace, L.y_shared) : nullptr, sg,
-                                  static_cast<uint16_t*>(output), s),
+  return hip_check(launch_combine(at<float>(workspace, L.y_routed), yr_parts, tokens * k * H, wout, iout, tokens, k, E,
+                                  H, layer->has_shared ? at<float>(workspace, L.y_shared) : nullptr, ys_parts,
+                                  tokens * H, sg, static_cast<uint16_t*>(output), s),
                    "combine launch");
 }
 
@@ -481,6 +662,10 @@ int uqm_set_option(int option, int64_t value) {
     case UQM_OPT_FUSED_ROUTED_BLOCKS:
       if (value < 0 || value > 4096) return fail(UQM_ERR_ARGUMENT, "routed workgroups must be in [0, 4096]");
       g_opt_fused_routed_blocks.store(value);
+      return UQM_OK;
+    case UQM_OPT_MFMA_MIN_TOKENS:
+      if (value < 0) return fail(UQM_ERR_ARGUMENT, "token threshold must be >= 0");
+      g_opt_mfma_min_tokens.store(value);
       return UQM_OK;
     default:
       return fail(UQM_ERR_ARGUMENT, "unknown option %d", option);

@@ -43,6 +43,38 @@ hipError_t launch_expert_gemv(int enc, int nmat, int mode, const GemvArgs& a, in
                               hipStream_t stream);
 size_t gemv_lds_bytes(int enc, int64_t K, int nt);
 
+// Expert-grouped GEMM on the MFMA cores (uqm_mfma.hip). Output block =
+// rows of one expert x one tile of up to 16*nb routes. Matrix m of expert e,
+// row r starts at w[m] + (e * rows + r) * row_bytes; scales as GemvArgs.
+struct MfmaArgs {
+  const uint8_t* w[2];
+  const float* s[2];
+  int64_t rows;  // output rows per expert (multiple of the workgroup's row block)
+  int64_t K;     // input features (multiple of 128)
+  int64_t group;
+  int64_t scales_per_expert;  // set by the launcher
+  const uint16_t* x;          // bf16 activations
+  int64_t ldx;
+  int32_t x_div;                  // activation row of route r is r / x_div
+  const int32_t* route_order;     // routes sorted by expert; null = identity
+  const int32_t* expert_offsets;  // [E+1] into route_order (with tiles)
+  const int32_t* tiles;           // [tile][2] = (expert, first index into route_order); null = one expert
+  const int32_t* tile_count;      // device count of tiles (with tiles)
+  int32_t tile_bound;             // tiles the grid covers (>= the device count)
+  int32_t n_routes;               // routes when tiles is null
+  void* out;                      // kModeSilu: bf16 [route, ldo]; kModeF32: fp32 [split][route, ldo]
+  int64_t ldo;
+  int64_t part_stride;  // elements between K-split partial outputs
+  int32_t ksplit;       // workgroups along K (kModeF32 only)
+  int32_t row_blocks;   // set by the launcher
+};
+
+bool mfma_supported(int enc, int64_t rows, int64_t K, int64_t group);
+// nmat 2 = gate/up with the SiLU epilogue (bf16 out), 1 = FP32 rows. nb: 16-route
+// tiles per workgroup (1, 2, 4; 8 for BF16); kw: waves along K (1 or 4, nb <= 2);
+// rt: 16-row tiles per wave (nmat 1, kw 1: 1 or 2).
+hipError_t launch_expert_mfma(int enc, int nmat, const MfmaArgs& a, int nb, int kw, int rt, hipStream_t stream);
+
 // Route tables produced on the device by the top-k / permutation kernels.
 struct RouteTables {
   int32_t* route_expert;    // [T*k] expert id per route (route = t*k + slot)
@@ -50,6 +82,8 @@ struct RouteTables {
   int32_t* expert_offsets;  // [E+1]
   int32_t* active_experts;  // [min(E, T*k)]
   int32_t* active_count;    // [1]
+  int32_t* tiles;           // [min(E, T*k) + T*k / tile_tokens][2] (optional)
+  int32_t* tile_count;      // [1]
 };
 
 // Top-k over bf16 logits [T, ldl] (columns 0..E-1), softmax in FP32, ties to
@@ -59,15 +93,18 @@ hipError_t launch_route_topk(const uint16_t* logits, int64_t ldl, int64_t T, int
                              uint16_t* weights_out, int64_t* indices_out, int32_t* route_expert,
                              float* shared_gate, hipStream_t stream);
 // Stable counting sort of the route expert table (invalid ids are dropped).
-// If order64/offsets64 are non-null, int64 copies are written too.
+// If order64/offsets64 are non-null, int64 copies are written too. With
+// tile_tokens > 0 it also lists, per expert in ascending id, its route tiles
+// of at most tile_tokens routes (rt.tiles, rt.tile_count).
 hipError_t launch_route_permute(const int32_t* route_expert, const int64_t* indices64, int64_t n_routes,
                                 int64_t E, const RouteTables& rt, int64_t* order64, int64_t* offsets64,
-                                hipStream_t stream);
+                                int tile_tokens, hipStream_t stream);
 
-// out[t, o] = bf16( sum_s w[t,s] * y[t*k+s, o] + sg[t] * ys[t, o] )
-hipError_t launch_combine(const float* y, const uint16_t* weights, const int64_t* indices, int64_t T, int64_t k,
-                          int64_t E, int64_t H, const float* ys, const float* sg, uint16_t* out,
-                          hipStream_t stream);
+// out[t, o] = bf16( sum_s w[t,s] * y[t*k+s, o] + sg[t] * ys[t, o] ), where y and
+// ys are the sums of y_parts / ys_parts FP32 partials spaced by *_stride elements.
+hipError_t launch_combine(const float* y, int y_parts, int64_t y_stride, const uint16_t* weights,
+                          const int64_t* indices, int64_t T, int64_t k, int64_t E, int64_t H, const float* ys,
+                          int ys_parts, int64_t ys_stride, const float* sg, uint16_t* out, hipStream_t stream);
 // Single-token fused MoE block (uqm_fused.hip). Sync words live in `sync`
 // (zero before the first launch): an epoch that the kernel advances on every
 // launch, a finished-workgroup counter it returns to zero, and a sticky error

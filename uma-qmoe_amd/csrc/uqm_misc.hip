@@ -14,10 +14,12 @@
 
 namespace uqm {
 
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, const uint16_t* __restrict__ w,
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, int y_parts, int64_t y_stride,
+                                                      const uint16_t* __restrict__ w,
                                                       const int64_t* __restrict__ idx, int64_t k, int64_t E,
-                                                      int64_t H, const float* __restrict__ ys,
-                                                      const float* __restrict__ sg, uint16_t* __restrict__ out) {
+                                                      int64_t H, const float* __restrict__ ys, int ys_parts,
+                                                      int64_t ys_stride, const float* __restrict__ sg,
+                                                      uint16_t* __restrict__ out) {
   const int64_t t = blockIdx.y;
   const int64_t o = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   if (o >= H) return;
@@ -26,7 +28,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     const int64_t e = idx[t * k + s];
     if (e < 0 || e >= E) continue;
     const float ws = bf16_to_f32(w[t * k + s]);
-    const float4 v = *reinterpret_cast<const float4*>(y + (t * k + s) * H + o);
+    float4 v = *reinterpret_cast<const float4*>(y + (t * k + s) * H + o);
+    for (int p = 1; p < y_parts; ++p) {
+      const float4 u = *reinterpret_cast<const float4*>(y + p * y_stride + (t * k + s) * H + o);
+      v.x += u.x;
+      v.y += u.y;
+      v.z += u.z;
+      v.w += u.w;
+    }
     acc.x = fmaf(ws, v.x, acc.x);
     acc.y = fmaf(ws, v.y, acc.y);
     acc.z = fmaf(ws, v.z, acc.z);
@@ -34,7 +43,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   }
   if (ys != nullptr) {
     const float g = sg[t];
-    const float4 v = *reinterpret_cast<const float4*>(ys + t * H + o);
+    float4 v = *reinterpret_cast<const float4*>(ys + t * H + o);
+    for (int p = 1; p < ys_parts; ++p) {
+      const float4 u = *reinterpret_cast<const float4*>(ys + p * ys_stride + t * H + o);
+      v.x += u.x;
+      v.y += u.y;
+      v.z += u.z;
+      v.w += u.w;
+    }
     acc.x = fmaf(g, v.x, acc.x);
     acc.y = fmaf(g, v.y, acc.y);
     acc.z = fmaf(g, v.z, acc.z);
@@ -45,12 +61,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   *reinterpret_cast<uint2*>(out + t * H + o) = make_uint2(lo, hi);
 }
 
-hipError_t launch_combine(const float* y, const uint16_t* weights, const int64_t* indices, int64_t T, int64_t k,
-                          int64_t E, int64_t H, const float* ys, const float* sg, uint16_t* out,
-                          hipStream_t stream) {
+hipError_t launch_combine(const float* y, int y_parts, int64_t y_stride, const uint16_t* weights,
+                          const int64_t* indices, int64_t T, int64_t k, int64_t E, int64_t H, const float* ys,
+                          int ys_parts, int64_t ys_stride, const float* sg, uint16_t* out, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>((H / 4 + 255) / 256), static_cast<unsigned>(T));
-  hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, stream, y, weights, indices, k, E, H, ys, sg, out);
+  hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, stream, y, y_parts, y_stride, weights, indices, k, E, H,
+                     ys, ys_parts, ys_stride, sg, out);
   return hipGetLastError();
 }
 

@@ -107,7 +107,9 @@ __global__ __launch_bounds__(64) void route_permute_kernel(const int32_t* __rest
                                                            int32_t* __restrict__ active_experts,
                                                            int32_t* __restrict__ active_count,
                                                            int64_t* __restrict__ order64,
-                                                           int64_t* __restrict__ offsets64) {
+                                                           int64_t* __restrict__ offsets64, int tile_tokens,
+                                                           int32_t* __restrict__ tiles,
+                                                           int32_t* __restrict__ tile_count) {
   __shared__ int cnt[256];
   __shared__ int run[256];
   const int lane = threadIdx.x;
@@ -136,6 +138,33 @@ __global__ __launch_bounds__(64) void route_permute_kernel(const int32_t* __rest
     if (lane >= o) incl += v;
   }
   int pre = incl - local;
+  if (tile_tokens > 0) {
+    // Route tiles: ceil(count / tile_tokens) per expert, in ascending expert id.
+    int nt4[4];
+    int tl = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      nt4[i] = (c4[i] + tile_tokens - 1) / tile_tokens;
+      tl += nt4[i];
+    }
+    int tincl = tl;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(tincl, o, kWave);
+      if (lane >= o) tincl += v;
+    }
+    int tpos = tincl - tl;
+    int first = pre;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      for (int j = 0; j < nt4[i]; ++j, ++tpos) {
+        tiles[2 * tpos] = 4 * lane + i;
+        tiles[2 * tpos + 1] = first + j * tile_tokens;
+      }
+      first += c4[i];
+    }
+    if (lane == 63) *tile_count = tincl;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = 4 * lane + i;
@@ -191,10 +220,11 @@ __global__ __launch_bounds__(64) void route_permute_kernel(const int32_t* __rest
 
 hipError_t launch_route_permute(const int32_t* route_expert, const int64_t* indices64, int64_t n_routes,
                                 int64_t E, const RouteTables& rt, int64_t* order64, int64_t* offsets64,
-                                hipStream_t stream) {
+                                int tile_tokens, hipStream_t stream) {
+  if (tile_tokens > 0 && (rt.tiles == nullptr || rt.tile_count == nullptr)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(route_permute_kernel, dim3(1), dim3(64), 0, stream, route_expert, indices64, n_routes,
                      static_cast<int>(E), rt.route_order, rt.expert_offsets, rt.active_experts, rt.active_count,
-                     order64, offsets64);
+                     order64, offsets64, tile_tokens, rt.tiles, rt.tile_count);
   return hipGetLastError();
 }
 
