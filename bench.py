@@ -37,8 +37,10 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=24)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2"])
-    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c4", "c5"],
+                    help="c2 (default): Qwen W4A16 decode; c1: OLMoE decode; c4: Qwen prefill, 512 tokens; "
+                         "c5: 128-expert top-8 layer, 256 tokens with Zipf-skewed routes (routed experts only)")
+    ap.add_argument("--tokens", type=int, default=0, help="tokens per call (0: the config's own)")
     ap.add_argument("--rotate-bytes", type=float, default=1.1e9)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -112,6 +114,28 @@ def profiled_traffic(workload: str):
     return int(data["traffic_bytes_per_launch"])
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
+
+
+def layer_flops(shape, tokens: int, routes: int) -> float:
+    """Multiply-adds x 2 of one block call: router, routed gate/up/down per
+    route, shared gate/up/down per token."""
+    f = 2.0 * shape.hidden * shape.num_experts * tokens
+    f += 6.0 * shape.hidden * shape.intermediate * routes
+    f += 6.0 * shape.hidden * shape.shared_intermediate * tokens
+    return f
+
+
+def zipf_routes(torch, syn, shape, x, dense):
+    """Top-k routes of a Zipf-biased router (c5): logits = bf16(x W_r^T + b).
+    Only the workload's routing pattern matters here, not tie order."""
+    bias = syn.zipf_router_bias(shape, 2.0, device=x.device)
+    vals = (torch.nn.functional.linear(x, dense.router).float() + bias).to(torch.bfloat16).float()
+    idx = torch.topk(vals, shape.top_k, dim=-1).indices
+    w = torch.softmax(vals, -1).gather(-1, idx).to(torch.bfloat16)
+    return idx.to(torch.int64).contiguous(), w.contiguous()
+
+
 def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
     """Times one MoE block call on `tokens` tokens: R distinct layer instances
     whose per-call reads together exceed `rotate_bytes` (>= 1 GB, so the 256 MB
@@ -122,12 +146,18 @@ def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
     expert)."""
     dev = torch.device("cuda:0")
     x = syn.hidden_states(shape, tokens, device=dev)
+    routed_only = shape.zipf_s is not None
     ws = ext._workspace(dev, tokens, shape.hidden, shape.intermediate, shape.shared_intermediate, shape.num_experts,
                         shape.top_k)
     probe = syn.build_experts(shape, device=dev, seed=syn.SEED)
     dense0 = syn.build_dense(shape, device=dev, seed=syn.SEED)
-    probe_idx = ext.moe_layer(probe, dense0, x, shape.top_k, workspace=ws)[3]
-    probe_bytes = syn.algorithmic_bytes(probe, dense0, int(torch.unique(probe_idx).numel()))
+    fixed = zipf_routes(torch, syn, shape, x, dense0) if routed_only else None
+    if routed_only:
+        probe_idx = fixed[0]
+        probe_bytes = syn.algorithmic_bytes(probe, None, int(torch.unique(probe_idx).numel()))
+    else:
+        probe_idx = ext.moe_layer(probe, dense0, x, shape.top_k, workspace=ws)[3]
+        probe_bytes = syn.algorithmic_bytes(probe, dense0, int(torch.unique(probe_idx).numel()))
     r_inst = max(2, math.ceil(rotate_bytes / probe_bytes))
     layers = [probe] + [syn.build_experts(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
     denses = [dense0] + [syn.build_dense(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
@@ -136,7 +166,11 @@ def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
     def run_all():
         res = []
         for i in range(r_inst):
-            res.append(ext.moe_layer(layers[i], denses[i], x, shape.top_k, out=outs[i], workspace=ws))
+            if routed_only:
+                ext.moe_forward(layers[i], x, fixed[0], fixed[1], out=outs[i], workspace=ws)
+                res.append((outs[i], None, fixed[1], fixed[0]))
+            else:
+                res.append(ext.moe_layer(layers[i], denses[i], x, shape.top_k, out=outs[i], workspace=ws))
         return res
 
     # eager warm-up, then capture the R calls in one graph
@@ -144,7 +178,12 @@ def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
         results = run_all()
     torch.cuda.synchronize()
     distinct = [int(torch.unique(res[3]).numel()) for res in results]
-    algo_bytes = [syn.algorithmic_bytes(layers[i], denses[i], distinct[i]) for i in range(r_inst)]
+    algo_bytes = [syn.algorithmic_bytes(layers[i], None if routed_only else denses[i], distinct[i])
+                  for i in range(r_inst)]
+    valid_routes = [int((res[3] >= 0).sum()) for res in results]
+    flops = sum(layer_flops(shape, tokens, r) for r in valid_routes) / r_inst
+    if routed_only:
+        flops -= 2.0 * shape.hidden * shape.num_experts * tokens  # the router is not run
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         run_all()
@@ -172,7 +211,21 @@ def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
     del graph, layers, denses, outs, ws
     torch.cuda.empty_cache()
     return {"us_per_layer": us, "gbps": mean_bytes / (us * 1e-6) / 1e9, "bytes": mean_bytes, "instances": r_inst,
-            "steps": n, "warmup": warm * r_inst}
+            "steps": n, "warmup": warm * r_inst, "flops": flops, "tflops": flops / (us * 1e-6) / 1e12,
+            "distinct_experts": sum(distinct) / len(distinct)}
+
+
+def workload_name(shape) -> str:
+    enc = {"q4_group128": "Q4", "q8_group128": "Q8", "bf16_le": "BF16"}[shape.encoding]
+    w = (f"{shape.name}: one MoE block (router + top-{shape.top_k} of {shape.num_experts} {enc} experts "
+         f"I={shape.intermediate}")
+    if shape.shared_intermediate:
+        w += f" + bf16 shared expert {shape.shared_intermediate}"
+    w += f"), H={shape.hidden}"
+    if shape.zipf_s is not None:
+        w = (f"{shape.name}: routed experts only, top-{shape.top_k} of {shape.num_experts} {enc} experts "
+             f"I={shape.intermediate}, H={shape.hidden}, Zipf(s={shape.zipf_s}) routes")
+    return w
 
 
 def main() -> int:
@@ -196,41 +249,49 @@ def main() -> int:
 
     _platform, ext = load_native_extension()
     shape = syn.CONFIGS[args.config]
-    head = measure(torch, syn, ext, shape, args.tokens, args.steps, args.warmup, args.rotate_bytes)
+    tokens = args.tokens if args.tokens > 0 else shape.tokens
+    head = measure(torch, syn, ext, shape, tokens, args.steps, args.warmup, args.rotate_bytes)
     us_per_layer = head["us_per_layer"]
     achieved = head["gbps"]
+    # the bound is whichever roofline leaves less time: HBM bytes or MFMA flops
+    mfma_bound = head["flops"] / (MFMA_PEAK_TFLOPS * 1e12) > head["bytes"] / (HBM_PEAK_GBPS * 1e9)
+    if mfma_bound:
+        roofline = {"bound": "mfma", "achieved": round(head["tflops"], 1), "peak": MFMA_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(head["tflops"] / MFMA_PEAK_TFLOPS, 4), "traffic": None}
+    else:
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                    "traffic": profiled_traffic(shape.name) if tokens == 1 else None}
     line = {
         "metric": BASELINE_METRIC,
-        "value": round(us_per_layer, 3),
+        "value": round(us_per_layer / tokens, 3),
         "unit": "us/token",
         "n_gpus": 1,
         "steps": head["steps"],
         "warmup": head["warmup"],
         "ms_per_step": round(us_per_layer / 1000.0, 6),
+        "us_per_layer_call": round(us_per_layer, 3),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "w4a16 (q4 weights, bf16 activations, fp32 accumulate)",
         "data": "synthetic (seeded N(0,0.02) weights, N(0,1) token)",
         "config": {
-            "workload": f"{shape.name}: one MoE block (router + top-{shape.top_k} of {shape.num_experts} Q4 experts "
-                        f"I={shape.intermediate} + bf16 shared expert {shape.shared_intermediate}), H={shape.hidden}",
-            "tokens": args.tokens,
+            "workload": workload_name(shape),
+            "tokens": tokens,
             "rotated_instances": head["instances"],
             "parallelism": "single GPU",
         },
-        "tokens_per_s": round(args.tokens / (us_per_layer * 1e-6), 1),
+        "tokens_per_s": round(tokens / (us_per_layer * 1e-6), 1),
         "algorithmic_bytes_per_call": int(head["bytes"]),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": profiled_traffic(shape.name) if args.tokens == 1 else None,
-        },
+        "hbm_gbps": round(achieved, 1),
+        "hbm_frac": round(achieved / HBM_PEAK_GBPS, 4),
+        "mfma_tflops": round(head["tflops"], 2),
+        "mfma_frac": round(head["tflops"] / MFMA_PEAK_TFLOPS, 4),
+        "distinct_experts": round(head["distinct_experts"], 2),
+        "roofline": roofline,
     }
-    if args.batch32 and args.tokens == 1:
+    if args.batch32 and tokens == 1 and args.config == "c2":
         b32 = measure(torch, syn, ext, shape, 32, max(32, args.steps // 4), max(8, args.warmup // 4), args.rotate_bytes)
         line["batch32"] = {
             "us_per_layer": round(b32["us_per_layer"], 3),
@@ -239,8 +300,9 @@ def main() -> int:
             "algorithmic_bytes_per_call": int(b32["bytes"]),
             "achieved_gbps": round(b32["gbps"], 1),
             "frac": round(b32["gbps"] / HBM_PEAK_GBPS, 4),
+            "distinct_experts": round(b32["distinct_experts"], 2),
         }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and tokens == 1:
         line["cpu_baseline"] = cpu_baseline(shape, args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0

@@ -104,7 +104,7 @@ int device_cus() {
 
 // Launch shape of one MFMA grouped GEMM (see launch_expert_mfma).
 struct MfmaPlan {
-  int nb = 1, kw = 1, rt = 1, ksplit = 1;
+  int nb = 1, kw = 1, mw = 4, ksplit = 1;
 };
 
 // 16-route tiles per workgroup from the mean routes per expert.
@@ -115,24 +115,24 @@ int nb_for(int enc, double mean_routes) {
   return 8;
 }
 
-// Enough workgroups to cover the chip: more rows per wave when there is
-// plenty of work, waves (then workgroups) along K when there is little.
-MfmaPlan plan_mfma(int nmat, int64_t rows, int64_t K, int nb, int64_t tiles, int cus, int max_split) {
+// Enough work items (row block x route tile) for the persistent grid: 8 MMA
+// waves (128 rows per item) when there is plenty of work, 4 (64 rows), then
+// waves and workgroups along K when there is little. Every K range keeps
+// >= 3 steps of 128 per wave.
+MfmaPlan plan_mfma(int enc, int nmat, int64_t rows, int64_t K, int nb, int64_t tiles, int cus, int max_split) {
   MfmaPlan p;
   p.nb = nb;
-  if (nmat == 2) {
-    if (nb <= 2 && rows / 64 * tiles < cus) p.kw = 4;
+  if (nb <= 2 && (nmat == 1 || enc == UQM_Q4) && rows % 128 == 0 && rows / 128 * tiles >= cus) {
+    p.mw = 8;
     return p;
   }
-  if (rows % 128 == 0 && rows / 128 * tiles >= 2 * cus) {
-    p.rt = 2;
-    return p;
-  }
-  if (rows / 64 * tiles >= cus) return p;
-  if (nb <= 2) p.kw = 4;
-  const int64_t wgs = rows / (p.kw == 4 ? 16 : 64) * tiles;
-  int64_t ks = (cus + wgs - 1) / wgs;
-  const int64_t max_by_k = (K / 128) / (2 * p.kw);  // keep >= 2 steps per wave
+  const int64_t items64 = rows / 64 * tiles;
+  if (items64 >= cus) return p;
+  if (nb == 1 && K / 128 >= 12) p.kw = 4;
+  if (nmat == 2) return p;
+  const int64_t items = rows / (p.kw == 4 ? 16 : 64) * tiles;
+  int64_t ks = (cus + items - 1) / items;
+  const int64_t max_by_k = (K / 128) / (3 * p.kw);
   if (ks > max_split) ks = max_split;
   if (ks > max_by_k) ks = max_by_k;
   p.ksplit = ks < 1 ? 1 : static_cast<int>(ks);
@@ -241,8 +241,8 @@ int run_routed(const uqm_expert_weights* w, const uint16_t* hidden, int64_t T, i
     g.out = at<uint16_t>(ws, L.h_routed);
     g.ldo = I;
     g.ksplit = 1;
-    const MfmaPlan pg = plan_mfma(2, I, H, nb, active, cus, 1);
-    int rc = hip_check(launch_expert_mfma(w->encoding, 2, g, pg.nb, pg.kw, pg.rt, stream), "gate/up MFMA launch");
+    const MfmaPlan pg = plan_mfma(w->encoding, 2, I, H, nb, active, cus, 1);
+    int rc = hip_check(launch_expert_mfma(w->encoding, 2, g, pg.nb, pg.kw, pg.mw, cus, stream), "gate/up MFMA launch");
     if (rc) return rc;
     MfmaArgs d = g;
     d.w[0] = static_cast<const uint8_t*>(w->down);
@@ -257,10 +257,10 @@ int run_routed(const uqm_expert_weights* w, const uint16_t* hidden, int64_t T, i
     d.out = at<float>(ws, L.y_routed);
     d.ldo = H;
     d.part_stride = R * H;
-    const MfmaPlan pd = plan_mfma(1, H, I, nb, active, cus, T > 1 ? kMaxSplit : 1);
+    const MfmaPlan pd = plan_mfma(w->encoding, 1, H, I, nb, active, cus, T > 1 ? kMaxSplit : 1);
     d.ksplit = pd.ksplit;
     *parts = pd.ksplit;
-    return hip_check(launch_expert_mfma(w->encoding, 1, d, pd.nb, pd.kw, pd.rt, stream), "down MFMA launch");
+    return hip_check(launch_expert_mfma(w->encoding, 1, d, pd.nb, pd.kw, pd.mw, cus, stream), "down MFMA launch");
   }
   const int grid_y = static_cast<int>(E < R ? E : R);
   const int nt = static_cast<int>(T < 4 ? T : 4);
@@ -323,8 +323,8 @@ int run_shared(const uqm_layer_weights* layer, const uint16_t* x, int64_t T, int
     g.out = at<uint16_t>(ws, L.h_shared);
     g.ldo = Is;
     g.ksplit = 1;
-    const MfmaPlan pg = plan_mfma(2, Is, H, nb, tiles, cus, 1);
-    int rc = hip_check(launch_expert_mfma(UQM_BF16, 2, g, pg.nb, pg.kw, pg.rt, stream), "shared gate/up MFMA launch");
+    const MfmaPlan pg = plan_mfma(UQM_BF16, 2, Is, H, nb, tiles, cus, 1);
+    int rc = hip_check(launch_expert_mfma(UQM_BF16, 2, g, pg.nb, pg.kw, pg.mw, cus, stream), "shared gate/up MFMA launch");
     if (rc) return rc;
     MfmaArgs d = g;
     d.w[0] = static_cast<const uint8_t*>(layer->shared_down);
@@ -336,10 +336,10 @@ int run_shared(const uqm_layer_weights* layer, const uint16_t* x, int64_t T, int
     d.out = at<float>(ws, L.y_shared);
     d.ldo = H;
     d.part_stride = T * H;
-    const MfmaPlan pd = plan_mfma(1, H, Is, nb, tiles, cus, T > 1 ? kMaxSplit : 1);
+    const MfmaPlan pd = plan_mfma(UQM_BF16, 1, H, Is, nb, tiles, cus, T > 1 ? kMaxSplit : 1);
     d.ksplit = pd.ksplit;
     *parts = pd.ksplit;
-    return hip_check(launch_expert_mfma(UQM_BF16, 1, d, pd.nb, pd.kw, pd.rt, stream), "shared down MFMA launch");
+    return hip_check(launch_expert_mfma(UQM_BF16, 1, d, pd.nb, pd.kw, pd.mw, cus, stream), "shared down MFMA launch");
   }
   const int nt = static_cast<int>(T < 4 ? T : 4);
   GemvArgs g{};

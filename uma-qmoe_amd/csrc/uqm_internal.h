@@ -71,9 +71,11 @@ struct MfmaArgs {
 
 bool mfma_supported(int enc, int64_t rows, int64_t K, int64_t group);
 // nmat 2 = gate/up with the SiLU epilogue (bf16 out), 1 = FP32 rows. nb: 16-route
-// tiles per workgroup (1, 2, 4; 8 for BF16); kw: waves along K (1 or 4, nb <= 2);
-// rt: 16-row tiles per wave (nmat 1, kw 1: 1 or 2).
-hipError_t launch_expert_mfma(int enc, int nmat, const MfmaArgs& a, int nb, int kw, int rt, hipStream_t stream);
+// tiles per work item (1, 2; 4 and (BF16) 8 with mw 4); kw: waves along K (1, or
+// 4 with nb 1 and mw 4); mw: MMA waves per workgroup (4 or 8; a work item covers
+// 16 * mw / kw rows); cus: compute units (the grid is persistent).
+hipError_t launch_expert_mfma(int enc, int nmat, const MfmaArgs& a, int nb, int kw, int mw, int cus,
+                              hipStream_t stream);
 
 // Route tables produced on the device by the top-k / permutation kernels.
 struct RouteTables {

@@ -5,59 +5,74 @@
 // for Q4, :781-1099 for Q8; launchers :1486-1641) and its BF16 grouped_mm path
 // (src/uma_qmoe/native_backend.py:958-1005), and serves the shared expert too.
 //
-// One workgroup = 4 waves computes an output block of (rows of one expert) x
-// (one tile of up to 16*NB routes of that expert):
-//   * weights go from HBM straight into MFMA A operands, each wave streaming
-//     its own rows through a ring of in-flight 16-byte loads; Q4 nibbles and
-//     Q8 bytes become exact bf16 integers (q + bias) in registers, so the
-//     MFMA sums x*(q + bias) over one 128-element group and the epilogue
-//     applies scale*(sum - bias*sum(x)) in FP32;
-//   * the routes' activations are gathered into LDS 128 K-elements at a time
-//     (double-buffered, prefetched one step ahead through registers) and read
-//     as MFMA B operands by every wave;
-//   * the 4 waves split the rows (WR = 4/KW row groups) and/or the K range
-//     (KW groups, partial sums combined through LDS at the end); whole
-//     workgroups can also split K (gridDim.y) and write FP32 partials that the
-//     combine kernel adds.
-// MFMA: v_mfma_f32_16x16x32_bf16. A lane l holds row l%16 / token l%16 and
-// K-slice 8*(l/16)..+7 of A / B; D lane l holds token l%16, rows 4*(l/16)+i.
-// The K elements a lane feeds each MFMA follow the order of its weight loads;
-// A and B use the same order, so the sum is unchanged.
+// One workgroup computes an output block of (rows of one expert) x (one tile
+// of up to 16*NB routes of that expert). It is split into producer and
+// consumer waves:
+//   * NL loader waves move every byte the step needs from global memory into
+//     LDS with global_load_lds (16 bytes per lane, no registers): the weight
+//     rows of the MMA waves and the gathered activations of the tile, for
+//     D steps ahead (a ring of D LDS buffers). Their only waits are their own
+//     vmcnt waits for the step about to be consumed, so the weight stream is
+//     never serialised behind anything else;
+//   * MW MMA waves (4 or 8) read A (weights) and B (activations) fragments from LDS and
+//     issue v_mfma_f32_16x16x32_bf16. Q4 nibbles and Q8 bytes become exact
+//     bf16 integers (q + bias) in registers, the MFMA sums x * (q + bias) over
+//     one 128-element scale group, and the epilogue applies
+//     scale * (sum - bias * sum(x)) in FP32 (sum(x) comes from the same B
+//     fragments via v_dot2 with ones). BF16 weights accumulate directly.
+// One s_barrier per step hands buffers between the two sides.
+//
+// The MMA waves split the rows (WR = MW/KW row groups) and/or the K range
+// (KW groups, partial sums combined through LDS at the end); whole workgroups
+// can also split K (gridDim.y) and write FP32 partials the combine kernel adds.
+//
+// MFMA operand layout (v_mfma_f32_16x16x32_bf16): A lane l holds row l%16 and
+// K-slice 8*(l/16)..+7; B lane l holds token l%16, same K-slice; D lane l
+// holds token l%16, rows 4*(l/16)+i. The K elements a lane feeds each MFMA
+// follow the order of its 16-byte weight slots; A and B use the same order,
+// so the sum is unchanged. Activation rows are stored in LDS with their
+// 16-byte slots XOR-swizzled by the token index, so the B reads of 16 tokens
+// hit distinct banks.
 //
 // Work tiles come from the device-built tile list (expert, first route); the
 // linear workgroup id is remapped so that each XCD (id % 8) walks a
 // contiguous range of (row block, tile) pairs with tiles fastest: the tiles
 // of one hot expert reuse the same weight rows through that XCD's L2.
+#include <atomic>
+#include <type_traits>
+
 #include "uqm_internal.h"
 
 namespace uqm {
 namespace {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) unsigned char lds_uchar_t;
 
 template <int ENC>
 struct MEnc;
 template <>
 struct MEnc<kQ4> {
-  static constexpr int kLoads = 1;        // 16-byte loads per lane per 128-element chunk
-  static constexpr int kChunkBytes = 64;  // bytes of one row's 128-element chunk
+  static constexpr int kChunk = 128;      // K elements per step (one scale group)
+  static constexpr int kLoads = 1;        // 16-byte slots per lane per step and A tile
+  static constexpr int kChunkBytes = 64;  // bytes of one row's chunk
   static constexpr float kBias = 136.0f;  // bf16(0x4300 | (nibble ^ 8)) = 136 + q
 };
 template <>
 struct MEnc<kQ8> {
+  static constexpr int kChunk = 128;
   static constexpr int kLoads = 2;
   static constexpr int kChunkBytes = 128;
   static constexpr float kBias = 128.0f;  // byte ^ 0x80 = q + 128
 };
 template <>
 struct MEnc<kBF16> {
-  static constexpr int kLoads = 4;
-  static constexpr int kChunkBytes = 256;
+  static constexpr int kChunk = 64;
+  static constexpr int kLoads = 2;
+  static constexpr int kChunkBytes = 128;
   static constexpr float kBias = 0.0f;
 };
-
-constexpr int kChunk = 128;         // K elements per step
-constexpr int kPitch = kChunk + 8;  // staged bf16 per token row; +16 B keeps ds_read_b128 conflict-free
 
 __device__ __forceinline__ uint32_t dw(const uint4& v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
@@ -68,21 +83,24 @@ __device__ __forceinline__ uint32_t hi16_pair(float lo, float hi) {
   return perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-// A operand (8 weights) of K-step S of a 128-element chunk.
-//   Q4: dword S of the lane's 16-byte load = elements 32q+8S .. +7
-//   Q8: load S/2, dwords 2(S%2), 2(S%2)+1 = elements 64(S/2)+16q+8(S%2) .. +7
-//   BF16: load S = elements 32S+8q .. +7
+// A operand (8 weights) of K-step S of a chunk from the lane's 16-byte slots.
+//   Q4: dword S of slot 0 = elements 32q+8S .. +7, as the bf16 pairs
+//       (e0,e4) (e1,e5) (e2,e6) (e3,e7); b_frag puts the activations in the
+//       same order
+
+//   Q8: slot S/2, dwords 2(S%2), 2(S%2)+1 = elements 64(S/2)+16q+8(S%2) .. +7
+//   BF16: slot S = elements 32S+8q .. +7
 template <int ENC, int S>
 __device__ __forceinline__ bf16x8_t a_frag(const uint4 (&v)[MEnc<ENC>::kLoads]) {
   u32x4_t o;
   if constexpr (ENC == kQ4) {
-    const uint32_t w = dw(v[0], S) ^ 0x88888888u;
-    const uint32_t lo = w & 0x0F0F0F0Fu;
-    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
-    o.x = perm(hi, lo, 0x0C040C00u) | 0x43004300u;
-    o.y = perm(hi, lo, 0x0C050C01u) | 0x43004300u;
-    o.z = perm(hi, lo, 0x0C060C02u) | 0x43004300u;
-    o.w = perm(hi, lo, 0x0C070C03u) | 0x43004300u;
+    // pair j = (element j, element j + 4) = nibbles j and j + 4, i.e. bits 4j
+    // and 16 + 4j: one masked xor/or per pair (a single v_bitop3)
+    const uint32_t w = dw(v[0], S);
+    o.x = ((w ^ 0x00080008u) & 0x000F000Fu) | 0x43004300u;
+    o.y = (((w >> 4) ^ 0x00080008u) & 0x000F000Fu) | 0x43004300u;
+    o.z = (((w >> 8) ^ 0x00080008u) & 0x000F000Fu) | 0x43004300u;
+    o.w = (((w >> 12) ^ 0x00080008u) & 0x000F000Fu) | 0x43004300u;
   } else if constexpr (ENC == kQ8) {
     const uint32_t d0 = dw(v[S >> 1], 2 * (S & 1)) ^ 0x80808080u;
     const uint32_t d1 = dw(v[S >> 1], 2 * (S & 1) + 1) ^ 0x80808080u;
@@ -99,8 +117,8 @@ __device__ __forceinline__ bf16x8_t a_frag(const uint4 (&v)[MEnc<ENC>::kLoads]) 
   return __builtin_bit_cast(bf16x8_t, o);
 }
 
-// Element offset (within a staged 128-element chunk) of the B operand of
-// K-step S for lane quadrant q, matching a_frag's order.
+// Element offset (within a chunk) of the B operand of K-step S for lane
+// quadrant q, matching a_frag's order.
 template <int ENC, int S>
 __device__ __forceinline__ int b_offset(int q) {
   if constexpr (ENC == kQ4) return 32 * q + 8 * S;
@@ -108,152 +126,261 @@ __device__ __forceinline__ int b_offset(int q) {
   else return 32 * S + 8 * q;
 }
 
-template <int ENC, int AT, int NB, int S>
-__device__ __forceinline__ void mfma_step(const uint4 (&w)[AT][MEnc<ENC>::kLoads], const uint16_t* xrow, int q,
-                                          f32x4_t (&d)[AT][NB]) {
-  bf16x8_t bfr[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-    bfr[b] = *reinterpret_cast<const bf16x8_t*>(xrow + b * 16 * kPitch + b_offset<ENC, S>(q));
-#pragma unroll
-  for (int ai = 0; ai < AT; ++ai) {
-    const bf16x8_t af = a_frag<ENC, S>(w[ai]);
-#pragma unroll
-    for (int b = 0; b < NB; ++b) d[ai][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[b], d[ai][b], 0, 0, 0);
+// B operand in the element order a_frag produces: natural pairs for Q8/BF16,
+// (x0,x4) (x1,x5) (x2,x6) (x3,x7) for Q4.
+template <int ENC>
+__device__ __forceinline__ bf16x8_t b_frag(bf16x8_t v) {
+  if constexpr (ENC == kQ4) {
+    const u32x4_t d = __builtin_bit_cast(u32x4_t, v);
+    u32x4_t o;
+    o.x = perm(d.z, d.x, 0x05040100u);
+    o.y = perm(d.z, d.x, 0x07060302u);
+    o.z = perm(d.w, d.y, 0x05040100u);
+    o.w = perm(d.w, d.y, 0x07060302u);
+    return __builtin_bit_cast(bf16x8_t, o);
+  } else {
+    return v;
   }
+}
+
+// s_waitcnt with only vmcnt limited (gfx9 encoding: vmcnt bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Waits until at most n * PER loads are outstanding (n < NMAX, wave-uniform).
+template <int PER, int NMAX>
+__device__ __forceinline__ void wait_vmcnt_steps(int n) {
+  if constexpr (NMAX > 1) {
+    if (n >= NMAX - 1) {
+      wait_vmcnt<(NMAX - 1) * PER>();
+      return;
+    }
+    wait_vmcnt_steps<PER, NMAX - 1>(n);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
+__device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(lds_dst), 16, 0, 0);
+}
+
+// Same, with the LDS destination as a (wave-uniform) LDS byte address.
+__device__ __forceinline__ void dma16_to(const void* src, uint32_t lds_addr) {
+  __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_void_t*>(static_cast<uintptr_t>(lds_addr)), 16, 0, 0);
 }
 
 }  // namespace
 
-template <int ENC, int NMAT, int RT, int NB, int KW, int MODE>
-__global__ __launch_bounds__(256) void expert_mfma_kernel(MfmaArgs a) {
+template <int ENC, int NMAT, int MW, int NB, int KW>
+struct MfmaCfg {
   using M = MEnc<ENC>;
-  constexpr int L = M::kLoads;
+  static constexpr int CH = M::kChunk;
+  static constexpr int L = M::kLoads;
+  static constexpr int KS = CH / 32;  // MFMA K-steps per chunk
+  static constexpr int AT = NMAT;     // 16-row A tiles per MMA wave (gate and up, or one)
+  static constexpr int WR = MW / KW;  // MMA waves along the rows
+  static constexpr int NTOK = 16 * NB;
+  static constexpr int WGR = 16 * WR;  // rows per work item (per matrix)
+  static constexpr int ROWB = CH * 2;       // bytes of one staged activation row
+  static constexpr int SPR = ROWB / 16;     // 16-byte slots per activation row
+  static constexpr int W_BYTES = MW * AT * L * 1024;
+  static constexpr int X_BYTES = KW * NTOK * ROWB;
+  static constexpr int BUF = W_BYTES + X_BYTES;
+  static constexpr int W_INSTR = MW * AT * L;  // 1 KB loads per step
+  static constexpr int X_INSTR = X_BYTES / 1024;
+  static constexpr int I_STEP = W_INSTR + X_INSTR;
+  static constexpr int D = BUF <= 12 * 1024 ? 6 : (BUF <= 32 * 1024 ? 4 : 3);
+  static constexpr int NL = (D - 2) * I_STEP > 63 ? 2 : 1;  // loader waves
+  static constexpr int I_WAVE = I_STEP / NL;
+  static constexpr int THREADS = 64 * (MW + NL);
+  static constexpr int SLOTS = 3;                      // item slots for the scales
+  static constexpr int MAX_ITEMS = NTOK <= 32 ? 32 : 16;  // work items per workgroup
+  static constexpr int META = 4 + NTOK;                // expert, first route, routes, row block, route ids
+  static constexpr int RED_BYTES = KW > 1 ? (KW - 1) * WR * AT * NB * 4 * 64 * 4 : 0;
+  static constexpr int FIXED_LDS = D * BUF + RED_BYTES + MAX_ITEMS * META * 4;
+  static_assert(W_INSTR % NL == 0 && X_INSTR % NL == 0, "loader waves share the step's loads evenly");
+  static_assert((D - 2) * I_WAVE <= 63, "outstanding loads per loader wave must fit vmcnt");
+  static_assert(X_BYTES % 1024 == 0, "activation tile must be whole 1 KB loads");
+  static_assert(D * BUF <= 144 * 1024, "LDS ring too large");
+};
+
+// Persistent workgroups: the (route tile, row block) work items are split into
+// 8 contiguous ranges, one per XCD (blockIdx % 8), and each XCD's range into
+// contiguous runs, one per workgroup. Items run row block fastest, so a
+// workgroup walks consecutive row blocks of one tile and the tiles of one hot
+// expert sit side by side in one XCD's range. A workgroup loads the metadata
+// of all its items into LDS once; after that its loader waves stream the
+// items' steps back to back through the LDS ring, and the MMA waves write each
+// item's outputs when its last step is done.
+template <int ENC, int NMAT, int MW, int NB, int KW, int MODE>
+__global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void expert_mfma_kernel(MfmaArgs a) {
+  using C = MfmaCfg<ENC, NMAT, MW, NB, KW>;
+  constexpr int RT = 1;
+  using M = typename C::M;
+  constexpr int CH = C::CH, L = C::L, KS = C::KS, AT = C::AT, WR = C::WR, NTOK = C::NTOK, WGR = C::WGR;
+  constexpr int D = C::D, NL = C::NL, SLOTS = C::SLOTS, META = C::META;
   constexpr bool kScaled = ENC != kBF16;
-  constexpr int AT = NMAT * RT;  // 16-row A tiles per wave
-  constexpr int WR = 4 / KW;     // waves along rows
-  constexpr int NTOK = 16 * NB;  // routes per tile
-  constexpr int WGR = 16 * RT * WR;  // rows per workgroup (per matrix)
-  constexpr int kRing = KW == 1 ? 16 : 8;                       // 16-byte weight loads in flight per lane
-  constexpr int P = (kRing / (AT * L)) > 1 ? (kRing / (AT * L)) : 1;  // weight steps in flight per wave
-  constexpr int NX = KW * NB;    // 16-byte activation loads per thread per step
-  constexpr int kBufElems = KW * NTOK * kPitch;
-  static_assert(KW == 1 || KW == 2 || KW == 4, "KW must divide the 4 waves");
-  static_assert(NMAT == 1 || RT == 1, "gate/up tiles use one 16-row tile per matrix");
+  static_assert(MW % KW == 0, "KW must divide the MMA waves");
 
   extern __shared__ __align__(16) unsigned char lds[];
-  uint16_t* xs = reinterpret_cast<uint16_t*>(lds);                          // [2][KW][NTOK][kPitch]
-  float* xsum = reinterpret_cast<float*>(lds + 2 * kBufElems * 2);           // [2][KW][NTOK]
-  float* scl = xsum + 2 * KW * NTOK;                                         // [NMAT][G][WGR]
+  float* red = reinterpret_cast<float*>(lds + D * C::BUF);
+  int* meta = reinterpret_cast<int*>(lds + D * C::BUF + C::RED_BYTES);
+  float* scl = reinterpret_cast<float*>(meta + C::MAX_ITEMS * META);  // [SLOTS][NMAT][WGR][G]
 
-  // ---- work tile (XCD-aware order: each XCD walks a contiguous range) ----
-  const unsigned per_xcd = gridDim.x >> 3;
-  const unsigned p = (blockIdx.x & 7u) * per_xcd + (blockIdx.x >> 3);
-  if (p >= static_cast<unsigned>(a.row_blocks) * static_cast<unsigned>(a.tile_bound)) return;
-  const int rblk = static_cast<int>(p / static_cast<unsigned>(a.tile_bound));
-  const int tile = static_cast<int>(p % static_cast<unsigned>(a.tile_bound));
-  int expert = 0, rbeg, nt;
-  if (a.tiles != nullptr) {
-    if (tile >= *a.tile_count) return;
-    expert = a.tiles[2 * tile];
-    rbeg = a.tiles[2 * tile + 1];
-    nt = min(NTOK, a.expert_offsets[expert + 1] - rbeg);
-  } else {
-    rbeg = tile * NTOK;
-    nt = min(NTOK, a.n_routes - rbeg);
-  }
-  if (nt <= 0) return;
+  // ---- this workgroup's run of work items ----
+  const int n_tiles = a.tiles != nullptr ? *a.tile_count : a.tile_bound;
+  const int n_items = a.row_blocks * n_tiles;
+  const int xcd = static_cast<int>(blockIdx.x & 7u);
+  const int per = static_cast<int>(gridDim.x >> 3);
+  const int wslot = static_cast<int>(blockIdx.x >> 3);
+  const int xb = static_cast<int>(static_cast<int64_t>(n_items) * xcd / 8);
+  const int xe = static_cast<int>(static_cast<int64_t>(n_items) * (xcd + 1) / 8);
+  const int ib = xb + static_cast<int>(static_cast<int64_t>(xe - xb) * wslot / per);
+  const int ie = xb + static_cast<int>(static_cast<int64_t>(xe - xb) * (wslot + 1) / per);
+  const int nit = min(ie - ib, C::MAX_ITEMS);  // the launcher sizes the grid so that ie - ib <= MAX_ITEMS
+  if (nit <= 0) return;
 
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int q = lane >> 4;
-  const int wr = wave % WR;
-  const int kw = wave / WR;
-
-  const int nch = static_cast<int>(a.K / kChunk);
+  const int nch = static_cast<int>(a.K / CH);
   const int cps = (nch + a.ksplit - 1) / a.ksplit;
   const int c_begin = blockIdx.y * cps;
   const int c_end = min(nch, c_begin + cps);
   if (c_begin >= c_end) return;  // uniform over the workgroup
-  const int steps = (c_end - c_begin + KW - 1) / KW;
+  const int S = (c_end - c_begin + KW - 1) / KW;  // steps per item
+  const int total = nit * S;
   const int G = kScaled ? static_cast<int>(a.K / a.group) : 0;  // scale groups per row
-  const int gdiv = kScaled ? static_cast<int>(a.group / kChunk) : 1;
-
-  const int64_t wg_row0 = static_cast<int64_t>(rblk) * WGR;
+  const int gdiv = kScaled ? static_cast<int>(a.group / CH) : 1;
   const int64_t row_bytes = ENC == kQ4 ? a.K / 2 : (ENC == kQ8 ? a.K : 2 * a.K);
 
-  // ---- per-lane weight pointers (A layout: row lane%16, 16-byte slot q) ----
-  const uint8_t* wp[AT];
-#pragma unroll
-  for (int ai = 0; ai < AT; ++ai) {
-    const int m = NMAT == 2 ? ai : 0;
-    const int rt = NMAT == 2 ? 0 : ai;
-    const int64_t row = wg_row0 + wr * 16 * RT + rt * 16 + (lane & 15);
-    wp[ai] = a.w[m] + (static_cast<int64_t>(expert) * a.rows + row) * row_bytes + q * 16;
-  }
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
 
-  // ---- scales of the workgroup's rows into LDS, transposed to [m][g][row] ----
-  if constexpr (kScaled) {
-    for (int idx = tid; idx < NMAT * WGR * G; idx += 256) {
-      const int g = idx % G;
-      const int rr = (idx / G) % WGR;
-      const int m = idx / (G * WGR);
-      scl[(m * G + g) * WGR + rr] =
-          a.s[m][static_cast<int64_t>(expert) * a.scales_per_expert + (wg_row0 + rr) * G + g];
+  // ---- metadata of the run into LDS (every wave takes part in the barriers) ----
+  for (int i = tid; i < nit; i += C::THREADS) {
+    const int item = ib + i;
+    const int tile = item / a.row_blocks;
+    int expert = 0, rbeg, nt;
+    if (a.tiles != nullptr) {
+      expert = a.tiles[2 * tile];
+      rbeg = a.tiles[2 * tile + 1];
+      nt = min(NTOK, a.expert_offsets[expert + 1] - rbeg);
+    } else {
+      rbeg = tile * NTOK;
+      nt = min(NTOK, a.n_routes - rbeg);
     }
+    int* m = meta + i * META;
+    m[0] = expert;
+    m[1] = rbeg;
+    m[2] = nt;
+    m[3] = item - tile * a.row_blocks;
   }
-
-  // ---- activation rows this thread stages (fixed over the K loop) ----
-  const uint16_t* xp[NX];
-  bool xv[NX];
-#pragma unroll
-  for (int i = 0; i < NX; ++i) {
-    const int idx = tid + 256 * i;
-    const int tok = (idx >> 4) % NTOK;
-    xv[i] = tok < nt;
-    int route = rbeg + (xv[i] ? tok : 0);
+  __syncthreads();
+  for (int idx = tid; idx < nit * NTOK; idx += C::THREADS) {
+    const int i = idx / NTOK;
+    const int tok = idx - i * NTOK;
+    int* m = meta + i * META;
+    int route = m[1] + (tok < m[2] ? tok : 0);
     if (a.route_order != nullptr) route = a.route_order[route];
-    xp[i] = a.x + static_cast<int64_t>(route / a.x_div) * a.ldx + (idx & 15) * 8;
+    m[4 + tok] = route;
   }
-  auto load_x = [&](int j, uint4 (&r)[NX]) {
-#pragma unroll
-    for (int i = 0; i < NX; ++i) {
-      const int kwi = ((tid + 256 * i) >> 4) / NTOK;
-      const int c = c_begin + j * KW + kwi;
-      r[i] = (xv[i] && c < c_end) ? ldg16(xp[i] + static_cast<int64_t>(c) * kChunk) : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store_x = [&](int buf, const uint4 (&r)[NX]) {
-#pragma unroll
-    for (int i = 0; i < NX; ++i) {
-      const int idx = tid + 256 * i;
-      const int rowid = idx >> 4;  // kwi * NTOK + tok
-      *reinterpret_cast<uint4*>(xs + buf * kBufElems + rowid * kPitch + (idx & 15) * 8) = r[i];
-      if constexpr (kScaled) {
-        float s = bf16lo(r[i].x) + bf16hi(r[i].x) + bf16lo(r[i].y) + bf16hi(r[i].y) + bf16lo(r[i].z) +
-                  bf16hi(r[i].z) + bf16lo(r[i].w) + bf16hi(r[i].w);
-        s += xor_partner<8>(s);
-        s += xor_partner<4>(s);
-        s += xor_partner<2>(s);
-        s += xor_partner<1>(s);
-        if ((idx & 15) == 0) xsum[buf * KW * NTOK + rowid] = s;
-      }
-    }
-  };
+  __syncthreads();
 
-  // ---- weight ring ----
-  uint4 ring[P][AT][L];
-  auto load_w = [&](int j, uint4 (&slot)[AT][L]) {
-    const int c = c_begin + j * KW + kw;
-    if (c < c_end) {
+  if (wave >= MW) {
+    // =========================== loader waves ===========================
+    const int lw = NL == 1 ? 0 : wave - MW;
+    constexpr int XW = C::X_INSTR / NL;  // activation loads of this wave per step
+    const uint8_t* wrow[AT];  // this lane's row in A tile ai of MMA wave 0 (chunk 0 of the item)
+    const uint8_t* xsrc[XW];  // this lane's activation row slot of each of its activation loads
+    int xkw[XW];              // K group of the chunk an activation load feeds
+    int cur = -1;
+    auto setup_item = [&](int i) {
+      const int* m = meta + i * META;
+      const int expert = m[0];
+      const int64_t row0 = static_cast<int64_t>(m[3]) * WGR;
 #pragma unroll
-      for (int ai = 0; ai < AT; ++ai)
+      for (int ai = 0; ai < AT; ++ai) {
+        const int mat = NMAT == 2 ? ai : 0;
+        wrow[ai] = a.w[mat] + (static_cast<int64_t>(expert) * a.rows + row0 + (lane & 15)) * row_bytes + (lane >> 4) * 16;
+      }
 #pragma unroll
-        for (int u = 0; u < L; ++u)
-          slot[ai][u] = ldg16(wp[ai] + static_cast<int64_t>(c) * M::kChunkBytes + u * 64);
+      for (int k = 0; k < XW; ++k) {
+        const int xi = k * NL + lw;
+        const int r = xi * (1024 / C::ROWB) + lane / C::SPR;  // staged row = kwi * NTOK + tok
+        const int tok = r % NTOK;
+        const int slot = (lane % C::SPR) ^ (r & (C::SPR - 1));
+        const int route = m[4 + tok];
+        xsrc[k] = reinterpret_cast<const uint8_t*>(a.x + static_cast<int64_t>(route / a.x_div) * a.ldx) + slot * 16;
+        xkw[k] = r / NTOK;
+      }
+      if constexpr (kScaled) {
+        // the item's scales: per matrix one contiguous block of WGR rows x G groups
+        if (lw == 0) {
+          const int bytes = WGR * G * 4;
+          unsigned char* dst = reinterpret_cast<unsigned char*>(scl + (i % SLOTS) * NMAT * WGR * G);
+          for (int mat = 0; mat < NMAT; ++mat) {
+            const uint8_t* s_src =
+                reinterpret_cast<const uint8_t*>(a.s[mat] + static_cast<int64_t>(expert) * a.scales_per_expert + row0 * G);
+            for (int off = 0; off < bytes; off += 1024)
+              if (off + lane * 16 < bytes) dma16(s_src + off + lane * 16, dst + mat * bytes + off);
+          }
+        }
+      }
+    };
+    const int64_t wave_rows = 16 * row_bytes;  // bytes between the A tiles of adjacent MMA waves
+    const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_uchar_t*)(lds)));
+    auto issue = [&](int g) {
+      const int i = g / S;
+      const int sj = g - i * S;
+      if (i != cur) {
+        setup_item(i);
+        cur = i;
+      }
+      // LDS byte address of the step's buffer, kept wave-uniform (it goes to M0)
+      const uint32_t buf = __builtin_amdgcn_readfirstlane(lds_base + static_cast<uint32_t>((g % D) * C::BUF));
+      const int cb = c_begin + sj * KW;
+#pragma unroll
+      for (int k = 0; k < C::W_INSTR / NL; ++k) {
+        // (MMA wave, A tile, slot) of this load; compile-time when one wave loads
+        const int ii = k * NL + lw;
+        const int u = ii % L;
+        const int ai = (ii / L) % AT;
+        const int cw = ii / (L * AT);
+        const int c = min(cb + cw / WR, c_end - 1);
+        dma16_to(wrow[ai] + ((cw % WR) * wave_rows + static_cast<int64_t>(c) * M::kChunkBytes + u * 64),
+                 buf + ii * 1024);
+      }
+#pragma unroll
+      for (int k = 0; k < XW; ++k) {
+        const int c = min(cb + xkw[k], c_end - 1);
+        dma16_to(xsrc[k] + static_cast<int64_t>(c) * CH * 2, buf + C::W_BYTES + (k * NL + lw) * 1024);
+      }
+    };
+    // Loads complete in issue order, so "step s resident" = at most
+    // (steps issued after s) * I_WAVE loads outstanding; an item's scale loads
+    // are issued before its first step, so they only make the waits stricter.
+    for (int g = 0; g < min(D - 1, total); ++g) issue(g);
+    wait_vmcnt_steps<C::I_WAVE, D - 1>(min(D - 1, total) - 1);
+    __builtin_amdgcn_s_barrier();  // step 0 resident
+    for (int g = 0; g < total; ++g) {
+      if (g + D - 1 < total) issue(g + D - 1);
+      wait_vmcnt_steps<C::I_WAVE, D - 1>(max(0, min(total, g + D) - 1 - (g + 1)));
+      if constexpr (KW > 1) {
+        if (g % S == S - 1) __builtin_amdgcn_s_barrier();  // the MMA waves' partial-sum exchange
+      }
+      __builtin_amdgcn_s_barrier();  // step g consumed, step g+1 resident
     }
-  };
+    return;
+  }
+
+  // ============================= MMA waves =============================
+  const int q = lane >> 4;
+  const int wr = wave % WR;
+  const int kw = wave / WR;
+  const int t16 = lane & 15;
 
   f32x4_t acc[AT][NB];
 #pragma unroll
@@ -261,193 +388,264 @@ __global__ __launch_bounds__(256) void expert_mfma_kernel(MfmaArgs a) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[ai][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll
-  for (int j = 0; j < P; ++j)
-    if (j < steps) load_w(j, ring[j]);
-  uint4 xr[NX];
-  load_x(0, xr);
-  store_x(0, xr);
-  if (steps > 1) load_x(1, xr);
-  __syncthreads();
+  __syncthreads();  // step 0 resident
 
-  for (int j0 = 0; j0 < steps; j0 += P) {
+  for (int g = 0, i = 0, sj = 0; g < total; ++g) {
+    const int c = c_begin + sj * KW + kw;
+    if (c < c_end) {
+      const unsigned char* buf = lds + (g % D) * C::BUF;
+      uint4 wv[AT][L];
 #pragma unroll
-    for (int jj = 0; jj < P; ++jj) {
-      const int j = j0 + jj;
-      if (j >= steps) break;
-      const int buf = j & 1;
-      const int c = c_begin + j * KW + kw;
-      if (c < c_end) {
-        const uint16_t* xrow = xs + buf * kBufElems + (kw * NTOK + (lane & 15)) * kPitch;
-        if constexpr (kScaled) {
-          f32x4_t d[AT][NB];
+      for (int ai = 0; ai < AT; ++ai)
+#pragma unroll
+        for (int u = 0; u < L; ++u)
+          wv[ai][u] = *reinterpret_cast<const uint4*>(buf + ((wave * AT + ai) * L + u) * 1024 + lane * 16);
+      const unsigned char* xb = buf + C::W_BYTES + (kw * NTOK + t16) * C::ROWB;
+      f32x4_t d[AT][NB];
+      float xs[NB];
+      if constexpr (kScaled) {
+#pragma unroll
+        for (int ai = 0; ai < AT; ++ai)
+#pragma unroll
+          for (int b = 0; b < NB; ++b) d[ai][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int b = 0; b < NB; ++b) xs[b] = 0.f;
+      }
+      auto kstep = [&](auto s_tag) {
+        constexpr int S_ = decltype(s_tag)::value;
+        const int slot = (b_offset<ENC, S_>(q) >> 3) ^ (t16 & (C::SPR - 1));
+        bf16x8_t bfr[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          bfr[b] = b_frag<ENC>(*reinterpret_cast<const bf16x8_t*>(xb + b * 16 * C::ROWB + slot * 16));
+          if constexpr (kScaled) {
+            const u32x4_t bu = __builtin_bit_cast(u32x4_t, bfr[b]);
+            xs[b] = dot2(bu.x, 0x3F803F80u, xs[b]);
+            xs[b] = dot2(bu.y, 0x3F803F80u, xs[b]);
+            xs[b] = dot2(bu.z, 0x3F803F80u, xs[b]);
+            xs[b] = dot2(bu.w, 0x3F803F80u, xs[b]);
+          }
+        }
+#pragma unroll
+        for (int ai = 0; ai < AT; ++ai) {
+          const bf16x8_t af = a_frag<ENC, S_>(wv[ai]);
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            if constexpr (kScaled)
+              d[ai][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[b], d[ai][b], 0, 0, 0);
+            else
+              acc[ai][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[b], acc[ai][b], 0, 0, 0);
+          }
+        }
+      };
+      kstep(std::integral_constant<int, 0>{});
+      kstep(std::integral_constant<int, 1>{});
+      if constexpr (KS > 2) {
+        kstep(std::integral_constant<int, 2>{});
+        kstep(std::integral_constant<int, 3>{});
+      }
+      if constexpr (kScaled) {
+        // token t's chunk sum = sum over the 4 lane quadrants holding it
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          xs[b] += xor_partner<32>(xs[b]);
+          xs[b] += xor_partner<16>(xs[b]);
+          xs[b] *= M::kBias;
+        }
+        const int grp = c / gdiv;
+        const float* sc_item = scl + (i % SLOTS) * NMAT * WGR * G;
+#pragma unroll
+        for (int ai = 0; ai < AT; ++ai) {
+          const int mat = NMAT == 2 ? ai : 0;
+          const int rt = NMAT == 2 ? 0 : ai;
+          const float* sr = sc_item + (mat * WGR + wr * 16 * RT + rt * 16 + 4 * q) * G + grp;
+          const float s0 = sr[0], s1 = sr[G], s2 = sr[2 * G], s3 = sr[3 * G];
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            acc[ai][b][0] = fmaf(s0, d[ai][b][0] - xs[b], acc[ai][b][0]);
+            acc[ai][b][1] = fmaf(s1, d[ai][b][1] - xs[b], acc[ai][b][1]);
+            acc[ai][b][2] = fmaf(s2, d[ai][b][2] - xs[b], acc[ai][b][2]);
+            acc[ai][b][3] = fmaf(s3, d[ai][b][3] - xs[b], acc[ai][b][3]);
+          }
+        }
+      }
+    }
+    if (sj == S - 1) {
+      // ---- the item is complete: combine the K groups of waves, store ----
+      bool writer = true;
+      if constexpr (KW > 1) {
+        constexpr int kVals = AT * NB * 4;
+        if (kw > 0) {
 #pragma unroll
           for (int ai = 0; ai < AT; ++ai)
 #pragma unroll
-            for (int b = 0; b < NB; ++b) d[ai][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-          mfma_step<ENC, AT, NB, 0>(ring[jj], xrow, q, d);
-          mfma_step<ENC, AT, NB, 1>(ring[jj], xrow, q, d);
-          mfma_step<ENC, AT, NB, 2>(ring[jj], xrow, q, d);
-          mfma_step<ENC, AT, NB, 3>(ring[jj], xrow, q, d);
-          const int g = c / gdiv;
-          float xsv[NB];
+            for (int b = 0; b < NB; ++b)
 #pragma unroll
-          for (int b = 0; b < NB; ++b) xsv[b] = M::kBias * xsum[buf * KW * NTOK + kw * NTOK + b * 16 + (lane & 15)];
+              for (int e = 0; e < 4; ++e)
+                red[(((kw - 1) * WR + wr) * kVals + (ai * NB + b) * 4 + e) * 64 + lane] = acc[ai][b][e];
+        }
+        __syncthreads();
+        writer = kw == 0;
+        if (writer) {
 #pragma unroll
-          for (int ai = 0; ai < AT; ++ai) {
-            const int m = NMAT == 2 ? ai : 0;
-            const int rt = NMAT == 2 ? 0 : ai;
-            const float4 sc =
-                *reinterpret_cast<const float4*>(scl + (m * G + g) * WGR + wr * 16 * RT + rt * 16 + 4 * q);
+          for (int o = 1; o < KW; ++o)
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-              acc[ai][b][0] = fmaf(sc.x, d[ai][b][0] - xsv[b], acc[ai][b][0]);
-              acc[ai][b][1] = fmaf(sc.y, d[ai][b][1] - xsv[b], acc[ai][b][1]);
-              acc[ai][b][2] = fmaf(sc.z, d[ai][b][2] - xsv[b], acc[ai][b][2]);
-              acc[ai][b][3] = fmaf(sc.w, d[ai][b][3] - xsv[b], acc[ai][b][3]);
-            }
-          }
-        } else {
-          mfma_step<ENC, AT, NB, 0>(ring[jj], xrow, q, acc);
-          mfma_step<ENC, AT, NB, 1>(ring[jj], xrow, q, acc);
-          mfma_step<ENC, AT, NB, 2>(ring[jj], xrow, q, acc);
-          mfma_step<ENC, AT, NB, 3>(ring[jj], xrow, q, acc);
+            for (int ai = 0; ai < AT; ++ai)
+#pragma unroll
+              for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  acc[ai][b][e] += red[(((o - 1) * WR + wr) * kVals + (ai * NB + b) * 4 + e) * 64 + lane];
         }
       }
-      if (j + P < steps) load_w(j + P, ring[jj]);
-      if (j + 1 < steps) {
-        store_x(buf ^ 1, xr);
-        if (j + 2 < steps) load_x(j + 2, xr);
+      if (writer) {
+        const int* m = meta + i * META;
+        const int nt = m[2];
+        const int64_t row0 = static_cast<int64_t>(m[3]) * WGR;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int tok = b * 16 + t16;
+          if (tok >= nt) continue;
+          const int route = m[4 + tok];
+          if constexpr (MODE == kModeSilu) {
+            const int64_t r0 = row0 + wr * 16 + 4 * q;
+            uint16_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16(silu(round_bf16(acc[0][b][e])) * round_bf16(acc[1][b][e]));
+            const uint2 v = make_uint2(static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
+                                       static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16));
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + static_cast<int64_t>(route) * a.ldo + r0) = v;
+          } else {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+              const int64_t r0 = row0 + wr * 16 * RT + rt * 16 + 4 * q;
+              float* dst = reinterpret_cast<float*>(a.out) + blockIdx.y * a.part_stride +
+                           static_cast<int64_t>(route) * a.ldo + r0;
+              *reinterpret_cast<float4*>(dst) =
+                  make_float4(acc[rt][b][0], acc[rt][b][1], acc[rt][b][2], acc[rt][b][3]);
+            }
+          }
+        }
       }
-      __syncthreads();
-    }
-  }
-
-  // ---- combine the K groups of waves ----
-  if constexpr (KW > 1) {
-    float* red = reinterpret_cast<float*>(lds);
-    constexpr int kVals = AT * NB * 4;
-    if (kw > 0) {
 #pragma unroll
       for (int ai = 0; ai < AT; ++ai)
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            red[(((kw - 1) * WR + wr) * kVals + (ai * NB + b) * 4 + i) * 64 + lane] = acc[ai][b][i];
+        for (int b = 0; b < NB; ++b) acc[ai][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
-    __syncthreads();
-    if (kw != 0) return;
-#pragma unroll
-    for (int o = 1; o < KW; ++o)
-#pragma unroll
-      for (int ai = 0; ai < AT; ++ai)
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            acc[ai][b][i] += red[(((o - 1) * WR + wr) * kVals + (ai * NB + b) * 4 + i) * 64 + lane];
-  }
-
-  // ---- epilogue: D lane holds token lane%16 of each B tile, rows 4q..4q+3 ----
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    const int tok = b * 16 + (lane & 15);
-    if (tok >= nt) continue;
-    int route = rbeg + tok;
-    if (a.route_order != nullptr) route = a.route_order[route];
-    if constexpr (MODE == kModeSilu) {
-      const int64_t r0 = wg_row0 + wr * 16 + 4 * q;
-      uint16_t h[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) h[i] = f32_to_bf16(silu(round_bf16(acc[0][b][i])) * round_bf16(acc[1][b][i]));
-      const uint2 v = make_uint2(static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16),
-                                 static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16));
-      *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + static_cast<int64_t>(route) * a.ldo + r0) = v;
-    } else {
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const int64_t r0 = wg_row0 + wr * 16 * RT + rt * 16 + 4 * q;
-        float* dst = reinterpret_cast<float*>(a.out) + blockIdx.y * a.part_stride + static_cast<int64_t>(route) * a.ldo + r0;
-        *reinterpret_cast<float4*>(dst) = make_float4(acc[rt][b][0], acc[rt][b][1], acc[rt][b][2], acc[rt][b][3]);
-      }
+    if (++sj == S) {
+      sj = 0;
+      ++i;
     }
+    __syncthreads();  // step g consumed, step g+1 resident
   }
 }
 
 namespace {
 
-template <int ENC, int NMAT, int RT, int NB, int KW>
+template <int ENC, int NMAT, int MW, int NB, int KW>
 size_t lds_bytes_for(int64_t K, int64_t group) {
-  constexpr int NTOK = 16 * NB;
-  const size_t xs = 2ull * KW * NTOK * kPitch * 2 + 2ull * KW * NTOK * 4;
+  using C = MfmaCfg<ENC, NMAT, MW, NB, KW>;
   const size_t G = ENC == kBF16 ? 0 : static_cast<size_t>(K / group);
-  return xs + sizeof(float) * NMAT * G * (16 * RT * (4 / KW));
+  return static_cast<size_t>(C::FIXED_LDS) + sizeof(float) * C::SLOTS * NMAT * G * C::WGR;
 }
 
-template <int ENC, int NMAT, int RT, int NB, int KW>
-hipError_t launch_cfg(const MfmaArgs& args, hipStream_t stream) {
-  constexpr int WGR = 16 * RT * (4 / KW);
+// Workgroups of one configuration that fit on a CU (cached per LDS size).
+template <int ENC, int NMAT, int MW, int NB, int KW, int MODE>
+int blocks_per_cu(size_t lds) {
+  static std::atomic<int64_t> cache{-1};  // (lds << 8) | blocks
+  const int64_t c = cache.load(std::memory_order_relaxed);
+  if (c >= 0 && static_cast<size_t>(c >> 8) == lds) return static_cast<int>(c & 0xFF);
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, expert_mfma_kernel<ENC, NMAT, MW, NB, KW, MODE>,
+                                                   MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS, lds) != hipSuccess ||
+      n < 1)
+    n = 1;
+  if (n > 8) n = 8;
+  cache.store((static_cast<int64_t>(lds) << 8) | n, std::memory_order_relaxed);
+  return n;
+}
+
+template <int ENC, int NMAT, int MW, int NB, int KW>
+hipError_t launch_cfg(const MfmaArgs& args, int cus, hipStream_t stream) {
+  using C = MfmaCfg<ENC, NMAT, MW, NB, KW>;
   MfmaArgs a = args;
-  a.row_blocks = static_cast<int32_t>(a.rows / WGR);
-  const size_t lds = lds_bytes_for<ENC, NMAT, RT, NB, KW>(a.K, a.group);
+  a.row_blocks = static_cast<int32_t>(a.rows / C::WGR);
+  const int nch = static_cast<int>(a.K / C::CH);
+  const int steps = (nch / (a.ksplit > 0 ? a.ksplit : 1)) / KW;
+  if (2 * steps + 1 < C::D) return hipErrorInvalidValue;  // scale slots would be reused too early
+  const size_t lds = lds_bytes_for<ENC, NMAT, MW, NB, KW>(a.K, a.group);
   if (lds > 160 * 1024) return hipErrorInvalidValue;
-  const unsigned total = static_cast<unsigned>(a.row_blocks) * static_cast<unsigned>(a.tile_bound);
-  const unsigned grid = (total + 7u) & ~7u;
   constexpr int MODE = NMAT == 2 ? kModeSilu : kModeF32;
-  auto kernel = expert_mfma_kernel<ENC, NMAT, RT, NB, KW, MODE>;
+  auto kernel = expert_mfma_kernel<ENC, NMAT, MW, NB, KW, MODE>;
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kernel, dim3(grid, static_cast<unsigned>(a.ksplit)), dim3(256), lds, stream, a);
+  // persistent grid: every resident slot once, more only if a run would exceed MAX_ITEMS
+  const int64_t items = static_cast<int64_t>(a.row_blocks) * a.tile_bound;
+  int64_t grid = static_cast<int64_t>(cus) * blocks_per_cu<ENC, NMAT, MW, NB, KW, MODE>(lds);
+  const int64_t need = (items + C::MAX_ITEMS - 3) / (C::MAX_ITEMS - 2);
+  if (grid < need) grid = need;
+  if (grid > items) grid = items;
+  grid = (grid + 7) & ~static_cast<int64_t>(7);
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid), static_cast<unsigned>(a.ksplit)), dim3(C::THREADS), lds,
+                     stream, a);
   return hipGetLastError();
 }
 
-template <int ENC, int NMAT, int RT, int KW>
-hipError_t launch_nb(const MfmaArgs& a, int nb, hipStream_t stream) {
-  if (nb <= 1) return launch_cfg<ENC, NMAT, RT, 1, KW>(a, stream);
-  if (nb <= 2) return launch_cfg<ENC, NMAT, RT, 2, KW>(a, stream);
+template <int ENC, int NMAT, int MW, int KW>
+hipError_t launch_nb(const MfmaArgs& a, int nb, int cus, hipStream_t stream) {
+  if (nb <= 1) return launch_cfg<ENC, NMAT, MW, 1, KW>(a, cus, stream);
   if constexpr (KW == 1) {
-    if (nb <= 4 || ENC != kBF16) return launch_cfg<ENC, NMAT, RT, 4, KW>(a, stream);
-    if constexpr (ENC == kBF16) return launch_cfg<ENC, NMAT, RT, 8, KW>(a, stream);
+    if (nb <= 2) return launch_cfg<ENC, NMAT, MW, 2, KW>(a, cus, stream);
+    if constexpr (MW == 4) {
+      if (nb <= 4 || ENC != kBF16) return launch_cfg<ENC, NMAT, MW, 4, KW>(a, cus, stream);
+      if constexpr (ENC == kBF16) return launch_cfg<ENC, NMAT, MW, 8, KW>(a, cus, stream);
+    }
   }
   return hipErrorInvalidValue;
 }
 
 template <int ENC>
-hipError_t launch_enc(int nmat, const MfmaArgs& a, int nb, int kw, int rt, hipStream_t stream) {
+hipError_t launch_enc(int nmat, const MfmaArgs& a, int nb, int kw, int mw, int cus, hipStream_t stream) {
   if (nmat == 2) {
-    if (kw == 4) return launch_nb<ENC, 2, 1, 4>(a, nb, stream);
-    return launch_nb<ENC, 2, 1, 1>(a, nb, stream);
+    if (kw == 4) return launch_nb<ENC, 2, 4, 4>(a, nb, cus, stream);
+    if constexpr (ENC == kQ4) {  // Q8/BF16 gate+up tiles need too many registers for 8 MMA waves
+      if (mw == 8) return launch_nb<ENC, 2, 8, 1>(a, nb, cus, stream);
+    }
+    return launch_nb<ENC, 2, 4, 1>(a, nb, cus, stream);
   }
-  if (kw == 4) return launch_nb<ENC, 1, 1, 4>(a, nb, stream);
-  if (rt == 2) return launch_nb<ENC, 1, 2, 1>(a, nb, stream);
-  return launch_nb<ENC, 1, 1, 1>(a, nb, stream);
+  if (kw == 4) return launch_nb<ENC, 1, 4, 4>(a, nb, cus, stream);
+  if (mw == 8) return launch_nb<ENC, 1, 8, 1>(a, nb, cus, stream);
+  return launch_nb<ENC, 1, 4, 1>(a, nb, cus, stream);
 }
 
 }  // namespace
 
 bool mfma_supported(int enc, int64_t rows, int64_t K, int64_t group) {
-  if (rows <= 0 || rows % 64 != 0 || K <= 0 || K % kChunk != 0) return false;
+  if (rows <= 0 || rows % 64 != 0 || K < 768 || K % 128 != 0) return false;
   if (enc == kBF16) return true;
-  return group > 0 && group % kChunk == 0 && K % group == 0 && K / group <= 64;
+  return group > 0 && group % 128 == 0 && K % group == 0 && K / group <= 64;
 }
 
-hipError_t launch_expert_mfma(int enc, int nmat, const MfmaArgs& args, int nb, int kw, int rt, hipStream_t stream) {
+hipError_t launch_expert_mfma(int enc, int nmat, const MfmaArgs& args, int nb, int kw, int mw, int cus,
+                              hipStream_t stream) {
   MfmaArgs a = args;
   if (a.ksplit < 1) a.ksplit = 1;
   if (nmat == 2 && a.ksplit != 1) return hipErrorInvalidValue;
   if (kw != 1 && kw != 4) return hipErrorInvalidValue;
-  if (kw == 4 && nb > 2) return hipErrorInvalidValue;
-  const int wgr = 16 * (nmat == 2 ? 1 : rt) * (4 / kw);
+  if (mw != 4 && mw != 8) return hipErrorInvalidValue;
+  if (kw == 4 && (nb > 1 || mw != 4)) return hipErrorInvalidValue;
+  if (mw == 8 && nb > 2) return hipErrorInvalidValue;
+  const int wgr = 16 * mw / kw;
   if (a.rows % wgr != 0) return hipErrorInvalidValue;
   if (enc != kBF16) a.scales_per_expert = (a.rows * a.K + a.group - 1) / a.group;
   if (a.tile_bound <= 0) return hipSuccess;
-  if (enc == kQ4) return launch_enc<kQ4>(nmat, a, nb, kw, rt, stream);
-  if (enc == kQ8) return launch_enc<kQ8>(nmat, a, nb, kw, rt, stream);
-  return launch_enc<kBF16>(nmat, a, nb, kw, rt, stream);
+  if (cus < 8) cus = 8;
+  if (enc == kQ4) return launch_enc<kQ4>(nmat, a, nb, kw, mw, cus, stream);
+  if (enc == kQ8) return launch_enc<kQ8>(nmat, a, nb, kw, mw, cus, stream);
+  return launch_enc<kBF16>(nmat, a, nb, kw, mw, cus, stream);
 }
 
 }  // namespace uqm

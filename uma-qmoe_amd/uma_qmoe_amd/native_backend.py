@@ -143,14 +143,27 @@ class HipExtension:
 
         self.torch = torch
         self.lib = _native.library()
+        self._ws_lock = threading.Lock()
+        self._ws_cache: dict[tuple[int, int], Any] = {}
 
     # ------------------------------------------------------------ helpers --
     def _workspace(self, device, tokens, hidden, inter, shared_inter, experts, top_k):
+        """A zero-filled workspace of the size the library asks for, reused by
+        later calls on the same device and stream (stream order keeps them
+        from overlapping; the fused single-token kernel leaves its sync words
+        ready for the next call). It grows when a call needs more."""
         n = self.lib.uqm_moe_workspace_bytes(tokens, hidden, inter, shared_inter, experts, top_k)
         if n == 0:
             raise RuntimeError("invalid workspace shape")
-        # zero-filled: the fused single-token kernel keeps its sync words here
-        return self.torch.zeros(n, dtype=self.torch.uint8, device=device)
+        torch = self.torch
+        dev = torch.device(device)
+        key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream_handle(torch, dev))
+        with self._ws_lock:
+            ws = self._ws_cache.get(key)
+            if ws is None or ws.numel() < n:
+                ws = torch.zeros(n, dtype=torch.uint8, device=dev)
+                self._ws_cache[key] = ws
+            return ws
 
     def _check_hidden(self, hidden):
         torch = self.torch
@@ -218,7 +231,7 @@ class HipExtension:
         return logits, weights, indices
 
     # ------------------------------------------------------------ experts --
-    def moe_forward(self, layer: DeviceExperts, hidden, expert_indices, routing_weights):
+    def moe_forward(self, layer: DeviceExperts, hidden, expert_indices, routing_weights, *, out=None, workspace=None):
         torch = self.torch
         self._check_hidden(hidden)
         x = hidden.reshape(-1, layer.hidden_size).contiguous()
@@ -230,8 +243,10 @@ class HipExtension:
         k = expert_indices.shape[1]
         idx = expert_indices.to(torch.int64).contiguous()
         w = routing_weights.to(torch.bfloat16).contiguous()
-        out = torch.empty_like(x)
-        ws = self._workspace(x.device, t, layer.hidden_size, layer.intermediate_size, 0, layer.num_experts, k)
+        out = torch.empty_like(x) if out is None else out
+        ws = workspace
+        if ws is None:
+            ws = self._workspace(x.device, t, layer.hidden_size, layer.intermediate_size, 0, layer.num_experts, k)
         desc = layer.descriptor()
         rc = self.lib.uqm_moe_forward(ctypes.byref(desc), _ptr(x), t, _ptr(idx), _ptr(w), k, _ptr(out), _ptr(ws),
                                       ws.numel(), _stream_handle(torch, x.device))
