@@ -73,7 +73,7 @@ def test_repeat_and_grid_size_are_bit_identical(fused_default):
     layer = syn.build_experts(shape, device=DEV, seed=11)
     dense = syn.build_dense(shape, device=DEV, seed=11)
     x = syn.hidden_states(shape, 1, device=DEV, seed=11)
-    ws = hip_ext._workspace(DEV, 1, shape.hidden, shape.intermediate, shape.shared_intermediate,
+    ws = hip_ext.new_workspace(DEV, 1, shape.hidden, shape.intermediate, shape.shared_intermediate,
                             shape.num_experts, shape.top_k)
     first = _block(hip_ext, layer, dense, x, shape, ws)
     for _ in range(4):

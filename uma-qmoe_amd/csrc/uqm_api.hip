@@ -42,7 +42,7 @@ constexpr int kMaxSplit = 4;
 
 struct Layout {
   size_t fused_sync, fused_hs, fused_hr, fused_yr, counters, route_expert, route_order, expert_offsets, active_experts,
-      tiles, logits, weights, indices, sg, h_routed, y_routed, h_shared, y_shared, total;
+      tiles, logits, weights, indices, sg, router_part, h_routed, y_routed, h_shared, y_shared, total;
 };
 
 Layout layout(int64_t T, int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k) {
@@ -68,6 +68,7 @@ Layout layout(int64_t T, int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k)
   L.weights = take(2 * R);
   L.indices = take(8 * R);
   L.sg = take(4 * static_cast<size_t>(T));
+  L.router_part = take(T > 1 ? 4 * static_cast<size_t>(kMaxSplit) * T * ((E + 1 + 15) / 16 * 16) : 0);
   L.h_routed = take(2 * R * I);
   L.y_routed = take(4 * R * H * (T > 1 ? kMaxSplit : 1));
   L.h_shared = take(2 * static_cast<size_t>(T) * Is);
@@ -207,6 +208,51 @@ int check_lds(int enc, int64_t K, int nt) {
   if (uqm::gemv_lds_bytes(enc, K, nt) > 64 * 1024)
     return fail(UQM_ERR_ARGUMENT, "input features %lld exceed the decode kernel's LDS staging limit", (long long)K);
   return UQM_OK;
+}
+
+bool router_uses_mfma(int64_t H, int64_t T) {
+  const int64_t min_t = g_opt_mfma_min_tokens.load(std::memory_order_relaxed);
+  return min_t > 0 && T >= min_t && T > 1 && uqm::mfma_supported(UQM_BF16, 64, H, 0);
+}
+
+// Router on T > 1 tokens as an MFMA GEMM over the router rows (plus the shared
+// expert's gate row, appended as row E): FP32 partial logits in the
+// workspace, then top-k, which rounds their sum to bf16 like the router's
+// bf16 linear. logits (optional) receives the bf16 logits [T, E].
+int run_router_mfma(const void* router, const void* gate_row, int64_t E, const uint16_t* x, int64_t T, int64_t H,
+                    int64_t k, int norm, const Layout& L, void* ws, uint16_t* wout, int64_t* iout,
+                    int32_t* route_expert, float* sg, uint16_t* logits, hipStream_t stream) {
+  using namespace uqm;
+  const int64_t rows = E + (gate_row != nullptr ? 1 : 0);
+  const int64_t rp = (rows + 15) / 16 * 16;
+  const int64_t tiles = (T + 15) / 16;
+  const int cus = device_cus();
+  MfmaArgs r{};
+  r.w[0] = static_cast<const uint8_t*>(router);
+  r.w_tail = static_cast<const uint8_t*>(gate_row);
+  r.tail_from = E;
+  r.rows = rp;
+  r.rows_valid = rows;
+  r.K = H;
+  r.x = x;
+  r.ldx = H;
+  r.x_div = 1;
+  r.tile_bound = static_cast<int32_t>(tiles);
+  r.n_routes = static_cast<int32_t>(T);
+  r.out = at<float>(ws, L.router_part);
+  r.ldo = rp;
+  r.part_stride = T * rp;
+  const int64_t items = rp / 16 * tiles;
+  int64_t ks = (cus + items - 1) / items;
+  const int64_t max_by_k = (H / 64) / (3 * 4);  // >= 3 steps of 64 per wave
+  if (ks > kMaxSplit) ks = kMaxSplit;
+  if (ks > max_by_k) ks = max_by_k;
+  r.ksplit = ks < 1 ? 1 : static_cast<int>(ks);
+  int rc = hip_check(launch_expert_mfma(UQM_BF16, 1, r, 1, 4, 4, cus, stream), "router MFMA launch");
+  if (rc) return rc;
+  return hip_check(launch_route_topk_partials(at<float>(ws, L.router_part), r.ksplit, T * rp, rp, T, E, k, norm, wout,
+                                              iout, route_expert, sg, logits, stream),
+                   "top-k launch");
 }
 
 // Routed experts, given device route tables already built in the workspace
@@ -473,6 +519,10 @@ int uqm_router_topk(const void* hidden, int64_t tokens, int64_t hidden_size, con
   if (workspace == nullptr || workspace_bytes < L.total)
     return fail(UQM_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (router_uses_mfma(hidden_size, tokens))
+    return run_router_mfma(router, nullptr, num_experts, static_cast<const uint16_t*>(hidden), tokens, hidden_size,
+                           top_k, norm_topk_prob, L, workspace, static_cast<uint16_t*>(routing_weights),
+                           expert_indices, nullptr, nullptr, static_cast<uint16_t*>(logits), s);
   uint16_t* lg = logits != nullptr ? static_cast<uint16_t*>(logits) : at<uint16_t>(workspace, L.logits);
   GemvArgs a{};
   a.w[0] = static_cast<const uint8_t*>(router);
@@ -604,24 +654,7 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
     return hip_check(launch_moe_decode_fused(w->encoding, fa, static_cast<int>(nr), s), "fused block launch");
   }
 
-  // 1. router logits (+ shared-gate logit in column E)
-  uint16_t* lg = at<uint16_t>(workspace, L.logits);
-  GemvArgs r{};
-  r.w[0] = static_cast<const uint8_t*>(layer->router);
-  if (layer->has_shared) {
-    r.w_tail = static_cast<const uint8_t*>(layer->shared_expert_gate);
-    r.tail_from = E;
-  }
-  r.rows = rows_router;
-  r.K = H;
-  r.x = x;
-  r.ldx = H;
-  r.x_div = 1;
-  r.n_routes = static_cast<int32_t>(tokens);
-  r.out = lg;
-  r.ldo = rows_router;
-  if ((rc = hip_check(launch_expert_gemv(UQM_BF16, 1, kModeBF16, r, 1, nt, s), "router launch"))) return rc;
-  // 2. top-k + permutation
+  // 1-2. router logits (+ shared-gate logit in column E), top-k
   uint16_t* wout = routing_weights != nullptr ? static_cast<uint16_t*>(routing_weights) : at<uint16_t>(workspace, L.weights);
   int64_t* iout = expert_indices != nullptr ? expert_indices : at<int64_t>(workspace, L.indices);
   float* sg = layer->has_shared ? at<float>(workspace, L.sg) : nullptr;
@@ -629,14 +662,38 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
                  at<int32_t>(workspace, L.expert_offsets), at<int32_t>(workspace, L.active_experts),
                  at<int32_t>(workspace, L.counters), at<int32_t>(workspace, L.tiles),
                  at<int32_t>(workspace, L.counters) + 1};
-  if ((rc = hip_check(launch_route_topk(lg, rows_router, tokens, E, k, layer->norm_topk_prob, wout, iout,
-                                        rt.route_expert, sg, s),
-                      "top-k launch")))
-    return rc;
-  if (logits != nullptr) {
-    if ((rc = hip_check(hipMemcpy2DAsync(logits, 2 * E, lg, 2 * rows_router, 2 * E, tokens, hipMemcpyDeviceToDevice, s),
-                        "logits copy")))
+  if (router_uses_mfma(H, tokens)) {
+    if ((rc = run_router_mfma(layer->router, layer->has_shared ? layer->shared_expert_gate : nullptr, E, x, tokens, H,
+                              k, layer->norm_topk_prob, L, workspace, wout, iout, rt.route_expert, sg,
+                              static_cast<uint16_t*>(logits), s)))
       return rc;
+  } else {
+    uint16_t* lg = at<uint16_t>(workspace, L.logits);
+    GemvArgs r{};
+    r.w[0] = static_cast<const uint8_t*>(layer->router);
+    if (layer->has_shared) {
+      r.w_tail = static_cast<const uint8_t*>(layer->shared_expert_gate);
+      r.tail_from = E;
+    }
+    r.rows = rows_router;
+    r.K = H;
+    r.x = x;
+    r.ldx = H;
+    r.x_div = 1;
+    r.n_routes = static_cast<int32_t>(tokens);
+    r.out = lg;
+    r.ldo = rows_router;
+    if ((rc = hip_check(launch_expert_gemv(UQM_BF16, 1, kModeBF16, r, 1, nt, s), "router launch"))) return rc;
+    if ((rc = hip_check(launch_route_topk(lg, rows_router, tokens, E, k, layer->norm_topk_prob, wout, iout,
+                                          rt.route_expert, sg, s),
+                        "top-k launch")))
+      return rc;
+    if (logits != nullptr) {
+      if ((rc = hip_check(hipMemcpy2DAsync(logits, 2 * E, lg, 2 * rows_router, 2 * E, tokens, hipMemcpyDeviceToDevice,
+                                           s),
+                          "logits copy")))
+        return rc;
+    }
   }
   const int tile_tokens = routed_tile_tokens(w, tokens, k);
   if ((rc = hip_check(launch_route_permute(rt.route_expert, nullptr, tokens * k, E, rt, nullptr, nullptr, tile_tokens, s),

@@ -49,6 +49,13 @@ size_t gemv_lds_bytes(int enc, int64_t K, int nt);
 struct MfmaArgs {
   const uint8_t* w[2];
   const float* s[2];
+  // Optional (single row group per work item only, i.e. kw 4 with mw 4): rows
+  // >= rows_valid read row rows_valid - 1 (their outputs are padding), and rows
+  // >= tail_from of matrix 0 come from w_tail (the router's appended
+  // shared-expert gate row).
+  const uint8_t* w_tail;
+  int64_t tail_from;
+  int64_t rows_valid;  // 0 = rows
   int64_t rows;  // output rows per expert (multiple of the workgroup's row block)
   int64_t K;     // input features (multiple of 128)
   int64_t group;
@@ -91,6 +98,13 @@ struct RouteTables {
 // Top-k over bf16 logits [T, ldl] (columns 0..E-1), softmax in FP32, ties to
 // the lower expert id. Writes bf16 weights / int64 indices [T, k], the route
 // expert table, and (if shared_gate != null) sigmoid of column E.
+// launch_route_topk_partials takes the logits as `parts` FP32 partial sums
+// [parts][T][ldl] (pstride elements apart), rounds their sum to bf16 (the
+// router's bf16 output) and, if logits_out != null, stores it [T, E].
+hipError_t launch_route_topk_partials(const float* plog, int parts, int64_t pstride, int64_t ldl, int64_t T,
+                                      int64_t E, int64_t k, int norm, uint16_t* weights_out, int64_t* indices_out,
+                                      int32_t* route_expert, float* shared_gate, uint16_t* logits_out,
+                                      hipStream_t stream);
 hipError_t launch_route_topk(const uint16_t* logits, int64_t ldl, int64_t T, int64_t E, int64_t k, int norm,
                              uint16_t* weights_out, int64_t* indices_out, int32_t* route_expert,
                              float* shared_gate, hipStream_t stream);

@@ -304,7 +304,16 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
 #pragma unroll
       for (int ai = 0; ai < AT; ++ai) {
         const int mat = NMAT == 2 ? ai : 0;
-        wrow[ai] = a.w[mat] + (static_cast<int64_t>(expert) * a.rows + row0 + (lane & 15)) * row_bytes + (lane >> 4) * 16;
+        int64_t row = row0 + (lane & 15);
+        if constexpr (WR == 1) {
+          // clamped padding rows and the appended tail row (router + shared-expert gate)
+          if (a.rows_valid > 0 && row >= a.rows_valid) row = a.rows_valid - 1;
+          if (mat == 0 && a.w_tail != nullptr && row >= a.tail_from) {
+            wrow[ai] = a.w_tail + (row - a.tail_from) * row_bytes + (lane >> 4) * 16;
+            continue;
+          }
+        }
+        wrow[ai] = a.w[mat] + (static_cast<int64_t>(expert) * a.rows + row) * row_bytes + (lane >> 4) * 16;
       }
 #pragma unroll
       for (int k = 0; k < XW; ++k) {
@@ -640,6 +649,7 @@ hipError_t launch_expert_mfma(int enc, int nmat, const MfmaArgs& args, int nb, i
   if (mw == 8 && nb > 2) return hipErrorInvalidValue;
   const int wgr = 16 * mw / kw;
   if (a.rows % wgr != 0) return hipErrorInvalidValue;
+  if ((a.w_tail != nullptr || (a.rows_valid > 0 && a.rows_valid != a.rows)) && wgr != 16) return hipErrorInvalidValue;
   if (enc != kBF16) a.scales_per_expert = (a.rows * a.K + a.group - 1) / a.group;
   if (a.tile_bound <= 0) return hipSuccess;
   if (cus < 8) cus = 8;

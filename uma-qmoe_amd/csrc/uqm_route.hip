@@ -14,24 +14,37 @@
 
 namespace uqm {
 
-__global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restrict__ logits, int64_t ldl,
-                                                         int64_t T, int E, int k, int norm,
+// Logit of column e: the bf16 value itself, or the bf16 rounding of the sum of
+// the FP32 partials.
+__device__ __forceinline__ float logit_of(const uint16_t* row, const float* prow, int parts, int64_t pstride, int e) {
+  if (prow == nullptr) return bf16_to_f32(row[e]);
+  float v = prow[e];
+  for (int p = 1; p < parts; ++p) v += prow[p * pstride + e];
+  return round_bf16(v);
+}
+
+__global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restrict__ logits,
+                                                         const float* __restrict__ plog, int parts, int64_t pstride,
+                                                         int64_t ldl, int64_t T, int E, int k, int norm,
                                                          uint16_t* __restrict__ weights_out,
                                                          int64_t* __restrict__ indices_out,
                                                          int32_t* __restrict__ route_expert,
-                                                         float* __restrict__ shared_gate) {
+                                                         float* __restrict__ shared_gate,
+                                                         uint16_t* __restrict__ logits_out) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + wave;
   if (t >= T) return;
-  const uint16_t* row = logits + t * ldl;
+  const uint16_t* row = plog != nullptr ? nullptr : logits + t * ldl;
+  const float* prow = plog != nullptr ? plog + t * ldl : nullptr;
 
   float l[4];
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
-    l[i] = e < E ? bf16_to_f32(row[e]) : -INFINITY;
+    l[i] = e < E ? logit_of(row, prow, parts, pstride, e) : -INFINITY;
+    if (logits_out != nullptr && e < E) logits_out[t * E + e] = f32_to_bf16(l[i]);
     mx = fmaxf(mx, l[i]);
   }
 #pragma unroll
@@ -78,7 +91,8 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
     indices_out[t * k + lane] = my_e;
     if (route_expert != nullptr) route_expert[t * k + lane] = my_e;
   }
-  if (shared_gate != nullptr && lane == 0) shared_gate[t] = round_bf16(sigmoidf_(bf16_to_f32(row[E])));
+  if (shared_gate != nullptr && lane == 0)
+    shared_gate[t] = round_bf16(sigmoidf_(logit_of(row, prow, parts, pstride, E)));
 }
 
 hipError_t launch_route_topk(const uint16_t* logits, int64_t ldl, int64_t T, int64_t E, int64_t k, int norm,
@@ -86,8 +100,21 @@ hipError_t launch_route_topk(const uint16_t* logits, int64_t ldl, int64_t T, int
                              float* shared_gate, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
   const dim3 grid(static_cast<unsigned>((T + 3) / 4));
-  hipLaunchKernelGGL(route_topk_kernel, grid, dim3(256), 0, stream, logits, ldl, T, static_cast<int>(E),
-                     static_cast<int>(k), norm, weights_out, indices_out, route_expert, shared_gate);
+  hipLaunchKernelGGL(route_topk_kernel, grid, dim3(256), 0, stream, logits, nullptr, 1, int64_t{0}, ldl, T,
+                     static_cast<int>(E), static_cast<int>(k), norm, weights_out, indices_out, route_expert,
+                     shared_gate, nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_route_topk_partials(const float* plog, int parts, int64_t pstride, int64_t ldl, int64_t T,
+                                      int64_t E, int64_t k, int norm, uint16_t* weights_out, int64_t* indices_out,
+                                      int32_t* route_expert, float* shared_gate, uint16_t* logits_out,
+                                      hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((T + 3) / 4));
+  hipLaunchKernelGGL(route_topk_kernel, grid, dim3(256), 0, stream, nullptr, plog, parts, pstride, ldl, T,
+                     static_cast<int>(E), static_cast<int>(k), norm, weights_out, indices_out, route_expert,
+                     shared_gate, logits_out);
   return hipGetLastError();
 }
 

@@ -165,6 +165,13 @@ class HipExtension:
                 self._ws_cache[key] = ws
             return ws
 
+    def new_workspace(self, device, tokens, hidden, inter, shared_inter, experts, top_k):
+        """A fresh zero-filled workspace owned by the caller (not the shared cache)."""
+        n = self.lib.uqm_moe_workspace_bytes(tokens, hidden, inter, shared_inter, experts, top_k)
+        if n == 0:
+            raise RuntimeError("invalid workspace shape")
+        return self.torch.zeros(n, dtype=self.torch.uint8, device=device)
+
     def _check_hidden(self, hidden):
         torch = self.torch
         if hidden.dtype != torch.bfloat16:
