@@ -121,7 +121,8 @@ def test_q4_groups_crossing_rows(hip_ext):
 
 
 # ----------------------------------------------------------------- routing --
-@pytest.mark.parametrize("t,k,e", [(1, 4, 60), (5, 8, 64), (512, 4, 60), (256, 8, 128), (33, 2, 256)])
+@pytest.mark.parametrize("t,k,e", [(1, 4, 60), (5, 8, 64), (512, 4, 60), (256, 8, 128), (33, 2, 256), (384, 8, 128),
+                                   (1000, 4, 60)])
 def test_route_permute_is_a_stable_sort(hip_ext, t, k, e):
     note(f"permute t={t} k={k} e={e}")
     g = torch.Generator().manual_seed(t + k + e)
@@ -139,6 +140,13 @@ def test_route_permute_drops_invalid_ids(hip_ext):
     order, offsets = hip_ext.route_permute(idx.to(DEV), 8)
     ref_order, ref_offsets = om.route_permutation(idx, 8)
     assert ref_order == [4, 0, 3, 5] and ref_offsets == [0, 1, 1, 1, 3, 3, 4, 4, 4]
+    assert order.cpu()[: int(offsets[-1])].tolist() == ref_order
+    assert offsets.cpu().tolist() == ref_offsets
+    # many routes (the workgroup-parallel sort), ids out of range sprinkled in
+    g = torch.Generator().manual_seed(5)
+    idx = torch.randint(-3, 70, (700, 4), generator=g)
+    order, offsets = hip_ext.route_permute(idx.to(DEV), 64)
+    ref_order, ref_offsets = om.route_permutation(idx, 64)
     assert order.cpu()[: int(offsets[-1])].tolist() == ref_order
     assert offsets.cpu().tolist() == ref_offsets
 

@@ -18,8 +18,9 @@
 //     issue v_mfma_f32_16x16x32_bf16. Q4 nibbles and Q8 bytes become exact
 //     bf16 integers (q + bias) in registers, the MFMA sums x * (q + bias) over
 //     one 128-element scale group, and the epilogue applies
-//     scale * (sum - bias * sum(x)) in FP32 (sum(x) comes from the same B
-//     fragments via v_dot2 with ones). BF16 weights accumulate directly.
+//     scale * (sum - bias * sum(x)) in FP32 (sum(x) comes from one more MFMA
+//     of the same B fragments with a ones-matrix). BF16 weights accumulate
+//     directly.
 // One s_barrier per step hands buffers between the two sides.
 //
 // The MMA waves split the rows (WR = MW/KW row groups) and/or the K range
@@ -84,9 +85,7 @@ __device__ __forceinline__ uint32_t hi16_pair(float lo, float hi) {
 }
 
 // A operand (8 weights) of K-step S of a chunk from the lane's 16-byte slots.
-//   Q4: dword S of slot 0 = elements 32q+8S .. +7, as the bf16 pairs
-//       (e0,e4) (e1,e5) (e2,e6) (e3,e7); b_frag puts the activations in the
-//       same order
+//   Q4: dword S of slot 0 = elements 32q+8S .. +7
 
 //   Q8: slot S/2, dwords 2(S%2), 2(S%2)+1 = elements 64(S/2)+16q+8(S%2) .. +7
 //   BF16: slot S = elements 32S+8q .. +7
@@ -94,13 +93,15 @@ template <int ENC, int S>
 __device__ __forceinline__ bf16x8_t a_frag(const uint4 (&v)[MEnc<ENC>::kLoads]) {
   u32x4_t o;
   if constexpr (ENC == kQ4) {
-    // pair j = (element j, element j + 4) = nibbles j and j + 4, i.e. bits 4j
-    // and 16 + 4j: one masked xor/or per pair (a single v_bitop3)
+    // pair d = (element 2d, element 2d + 1) = low and high nibble of byte d:
+    // v_perm puts byte d of w at bits 0-7 and byte d of w >> 4 at bits 16-23,
+    // then one masked xor/or (a single v_bitop3) makes both bf16 values
     const uint32_t w = dw(v[0], S);
-    o.x = ((w ^ 0x00080008u) & 0x000F000Fu) | 0x43004300u;
-    o.y = (((w >> 4) ^ 0x00080008u) & 0x000F000Fu) | 0x43004300u;
-    o.z = (((w >> 8) ^ 0x00080008u) & 0x000F000Fu) | 0x43004300u;
-    o.w = (((w >> 12) ^ 0x00080008u) & 0x000F000Fu) | 0x43004300u;
+    const uint32_t h = w >> 4;
+    o.x = (perm(h, w, 0x0C040C00u) ^ 0x00080008u) & 0x000F000Fu | 0x43004300u;
+    o.y = (perm(h, w, 0x0C050C01u) ^ 0x00080008u) & 0x000F000Fu | 0x43004300u;
+    o.z = (perm(h, w, 0x0C060C02u) ^ 0x00080008u) & 0x000F000Fu | 0x43004300u;
+    o.w = (perm(h, w, 0x0C070C03u) ^ 0x00080008u) & 0x000F000Fu | 0x43004300u;
   } else if constexpr (ENC == kQ8) {
     const uint32_t d0 = dw(v[S >> 1], 2 * (S & 1)) ^ 0x80808080u;
     const uint32_t d1 = dw(v[S >> 1], 2 * (S & 1) + 1) ^ 0x80808080u;
@@ -124,23 +125,6 @@ __device__ __forceinline__ int b_offset(int q) {
   if constexpr (ENC == kQ4) return 32 * q + 8 * S;
   else if constexpr (ENC == kQ8) return 64 * (S >> 1) + 16 * q + 8 * (S & 1);
   else return 32 * S + 8 * q;
-}
-
-// B operand in the element order a_frag produces: natural pairs for Q8/BF16,
-// (x0,x4) (x1,x5) (x2,x6) (x3,x7) for Q4.
-template <int ENC>
-__device__ __forceinline__ bf16x8_t b_frag(bf16x8_t v) {
-  if constexpr (ENC == kQ4) {
-    const u32x4_t d = __builtin_bit_cast(u32x4_t, v);
-    u32x4_t o;
-    o.x = perm(d.z, d.x, 0x05040100u);
-    o.y = perm(d.z, d.x, 0x07060302u);
-    o.z = perm(d.w, d.y, 0x05040100u);
-    o.w = perm(d.w, d.y, 0x07060302u);
-    return __builtin_bit_cast(bf16x8_t, o);
-  } else {
-    return v;
-  }
 }
 
 // s_waitcnt with only vmcnt limited (gfx9 encoding: vmcnt bits 3:0 and 15:14).
@@ -390,6 +374,7 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
   const int wr = wave % WR;
   const int kw = wave / WR;
   const int t16 = lane & 15;
+  const bf16x8_t kOnes = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
 
   f32x4_t acc[AT][NB];
 #pragma unroll
@@ -411,14 +396,14 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
           wv[ai][u] = *reinterpret_cast<const uint4*>(buf + ((wave * AT + ai) * L + u) * 1024 + lane * 16);
       const unsigned char* xb = buf + C::W_BYTES + (kw * NTOK + t16) * C::ROWB;
       f32x4_t d[AT][NB];
-      float xs[NB];
+      f32x4_t xs[NB];
       if constexpr (kScaled) {
 #pragma unroll
         for (int ai = 0; ai < AT; ++ai)
 #pragma unroll
           for (int b = 0; b < NB; ++b) d[ai][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int b = 0; b < NB; ++b) xs[b] = 0.f;
+        for (int b = 0; b < NB; ++b) xs[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
       auto kstep = [&](auto s_tag) {
         constexpr int S_ = decltype(s_tag)::value;
@@ -426,14 +411,10 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
         bf16x8_t bfr[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-          bfr[b] = b_frag<ENC>(*reinterpret_cast<const bf16x8_t*>(xb + b * 16 * C::ROWB + slot * 16));
-          if constexpr (kScaled) {
-            const u32x4_t bu = __builtin_bit_cast(u32x4_t, bfr[b]);
-            xs[b] = dot2(bu.x, 0x3F803F80u, xs[b]);
-            xs[b] = dot2(bu.y, 0x3F803F80u, xs[b]);
-            xs[b] = dot2(bu.z, 0x3F803F80u, xs[b]);
-            xs[b] = dot2(bu.w, 0x3F803F80u, xs[b]);
-          }
+          bfr[b] = *reinterpret_cast<const bf16x8_t*>(xb + b * 16 * C::ROWB + slot * 16);
+          // the chunk's activation sums on the matrix cores: a ones-matrix A
+          // puts sum_k x[k][t] in every row of column t
+          if constexpr (kScaled) xs[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kOnes, bfr[b], xs[b], 0, 0, 0);
         }
 #pragma unroll
         for (int ai = 0; ai < AT; ++ai) {
@@ -454,13 +435,9 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
         kstep(std::integral_constant<int, 3>{});
       }
       if constexpr (kScaled) {
-        // token t's chunk sum = sum over the 4 lane quadrants holding it
+        float xsb[NB];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          xs[b] += xor_partner<32>(xs[b]);
-          xs[b] += xor_partner<16>(xs[b]);
-          xs[b] *= M::kBias;
-        }
+        for (int b = 0; b < NB; ++b) xsb[b] = M::kBias * xs[b][0];
         const int grp = c / gdiv;
         const float* sc_item = scl + (i % SLOTS) * NMAT * WGR * G;
 #pragma unroll
@@ -471,10 +448,10 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
           const float s0 = sr[0], s1 = sr[G], s2 = sr[2 * G], s3 = sr[3 * G];
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
-            acc[ai][b][0] = fmaf(s0, d[ai][b][0] - xs[b], acc[ai][b][0]);
-            acc[ai][b][1] = fmaf(s1, d[ai][b][1] - xs[b], acc[ai][b][1]);
-            acc[ai][b][2] = fmaf(s2, d[ai][b][2] - xs[b], acc[ai][b][2]);
-            acc[ai][b][3] = fmaf(s3, d[ai][b][3] - xs[b], acc[ai][b][3]);
+            acc[ai][b][0] = fmaf(s0, d[ai][b][0] - xsb[b], acc[ai][b][0]);
+            acc[ai][b][1] = fmaf(s1, d[ai][b][1] - xsb[b], acc[ai][b][1]);
+            acc[ai][b][2] = fmaf(s2, d[ai][b][2] - xsb[b], acc[ai][b][2]);
+            acc[ai][b][3] = fmaf(s3, d[ai][b][3] - xsb[b], acc[ai][b][3]);
           }
         }
       }

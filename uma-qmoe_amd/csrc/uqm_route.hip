@@ -6,10 +6,10 @@
 // logits; weights are cast to BF16 (optionally renormalised first).
 //
 // The permutation replaces the reference's argsort(stable)/bincount/cumsum
-// (src/uma_qmoe/native_backend.py:530-543) with a single-wave stable counting
-// sort: per 64-route chunk, eight wave ballots give every lane the mask of
-// lanes holding the same expert id, so ranks come from one popcount and no
-// comparison sort is needed.
+// (src/uma_qmoe/native_backend.py:530-543) with a stable counting sort: per
+// 64-route chunk, eight wave ballots give every lane the mask of lanes holding
+// the same expert id, so ranks come from one popcount and no comparison sort
+// is needed (one workgroup up to 3072 routes, one wavefront beyond).
 #include "uqm_internal.h"
 
 namespace uqm {
@@ -126,30 +126,13 @@ __device__ __forceinline__ int load_route_id(const int32_t* route_expert, const 
   return valid ? static_cast<int>(id) : 0;
 }
 
-// One wavefront; E <= 256.
-__global__ __launch_bounds__(64) void route_permute_kernel(const int32_t* __restrict__ route_expert,
-                                                           const int64_t* __restrict__ indices64, int64_t n,
-                                                           int E, int32_t* __restrict__ route_order,
-                                                           int32_t* __restrict__ expert_offsets,
-                                                           int32_t* __restrict__ active_experts,
-                                                           int32_t* __restrict__ active_count,
-                                                           int64_t* __restrict__ order64,
-                                                           int64_t* __restrict__ offsets64, int tile_tokens,
-                                                           int32_t* __restrict__ tiles,
-                                                           int32_t* __restrict__ tile_count) {
-  __shared__ int cnt[256];
-  __shared__ int run[256];
-  const int lane = threadIdx.x;
-  for (int e = lane; e < 256; e += 64) cnt[e] = 0;
-  __syncthreads();
-
-  for (int64_t base = 0; base < n; base += 64) {
-    bool valid;
-    const int id = load_route_id(route_expert, indices64, base + lane, n, E, valid);
-    if (valid) atomicAdd(&cnt[id], 1);
-  }
-  __syncthreads();
-
+// Per-expert tables from the counts cnt[0..255] (one wavefront): exclusive
+// offsets into start[] (LDS) and expert_offsets[E+1], the route tiles (when
+// tile_tokens > 0) and the compact list of experts that have routes.
+__device__ void expert_tables(const int* cnt, int* start, int lane, int E, int32_t* __restrict__ expert_offsets,
+                              int64_t* __restrict__ offsets64, int tile_tokens, int32_t* __restrict__ tiles,
+                              int32_t* __restrict__ tile_count, int32_t* __restrict__ active_experts,
+                              int32_t* __restrict__ active_count) {
   // Exclusive scan over 4 experts per lane.
   int c4[4];
   int local = 0;
@@ -199,7 +182,7 @@ __global__ __launch_bounds__(64) void route_permute_kernel(const int32_t* __rest
       expert_offsets[e] = pre;
       if (offsets64 != nullptr) offsets64[e] = pre;
     }
-    run[e] = pre;
+    start[e] = pre;
     pre += c4[i];
   }
   const int total = __shfl(incl, 63, kWave);
@@ -207,6 +190,55 @@ __global__ __launch_bounds__(64) void route_permute_kernel(const int32_t* __rest
     expert_offsets[E] = total;
     if (offsets64 != nullptr) offsets64[E] = total;
   }
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int acc = 0;
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    const bool on = e < E && cnt[e] > 0;
+    const uint64_t m = __ballot(on);
+    if (on) active_experts[acc + __popcll(m & lt)] = e;
+    acc += __popcll(m);
+  }
+  if (lane == 0) *active_count = acc;
+}
+
+// Mask of the lanes of this wavefront that hold the same expert id (valid
+// ids only): one ballot per id bit.
+__device__ __forceinline__ uint64_t same_id_lanes(int id, bool valid, int nbits) {
+  uint64_t eq = __ballot(valid);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (id >> b) & 1;
+    const uint64_t bal = __ballot(bit);
+    eq &= bit ? bal : ~bal;
+  }
+  return eq;
+}
+
+// One wavefront; E <= 256. Any number of routes.
+__global__ __launch_bounds__(64) void route_permute_kernel(const int32_t* __restrict__ route_expert,
+                                                           const int64_t* __restrict__ indices64, int64_t n,
+                                                           int E, int32_t* __restrict__ route_order,
+                                                           int32_t* __restrict__ expert_offsets,
+                                                           int32_t* __restrict__ active_experts,
+                                                           int32_t* __restrict__ active_count,
+                                                           int64_t* __restrict__ order64,
+                                                           int64_t* __restrict__ offsets64, int tile_tokens,
+                                                           int32_t* __restrict__ tiles,
+                                                           int32_t* __restrict__ tile_count) {
+  __shared__ int cnt[256];
+  __shared__ int run[256];
+  const int lane = threadIdx.x;
+  for (int e = lane; e < 256; e += 64) cnt[e] = 0;
+  __syncthreads();
+
+  for (int64_t base = 0; base < n; base += 64) {
+    bool valid;
+    const int id = load_route_id(route_expert, indices64, base + lane, n, E, valid);
+    if (valid) atomicAdd(&cnt[id], 1);
+  }
+  __syncthreads();
+  expert_tables(cnt, run, lane, E, expert_offsets, offsets64, tile_tokens, tiles, tile_count, active_experts,
+                active_count);
   __syncthreads();
 
   int nbits = 1;
@@ -215,12 +247,7 @@ __global__ __launch_bounds__(64) void route_permute_kernel(const int32_t* __rest
   for (int64_t base = 0; base < n; base += 64) {
     bool valid;
     const int id = load_route_id(route_expert, indices64, base + lane, n, E, valid);
-    uint64_t eq = __ballot(valid);
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = (id >> b) & 1;
-      const uint64_t bal = __ballot(bit);
-      eq &= bit ? bal : ~bal;
-    }
+    const uint64_t eq = same_id_lanes(id, valid, nbits);
     const int rank = __popcll(eq & lt);
     int start = 0;
     if (valid) start = run[id];
@@ -233,25 +260,94 @@ __global__ __launch_bounds__(64) void route_permute_kernel(const int32_t* __rest
     }
     __syncthreads();
   }
+}
 
-  int acc = 0;
-  for (int e0 = 0; e0 < E; e0 += 64) {
-    const int e = e0 + lane;
-    const bool on = e < E && cnt[e] > 0;
-    const uint64_t m = __ballot(on);
-    if (on) active_experts[acc + __popcll(m & lt)] = e;
-    acc += __popcll(m);
+// One workgroup of 16 wavefronts for up to kPermuteMaxRoutes routes: the
+// routes are cut into 64-route chunks; every chunk's per-expert counts go to
+// an LDS histogram (ballot matching gives each route its rank inside its
+// chunk), a scan over the chunks per expert turns them into chunk bases, and
+// each route lands at offset[e] + base[chunk][e] + rank. Same stable order
+// as the one-wave kernel.
+constexpr int kPermuteMaxRoutes = 3072;
+constexpr int kPermuteWaves = 16;
+
+__global__ __launch_bounds__(64 * kPermuteWaves) void route_permute_wg_kernel(
+    const int32_t* __restrict__ route_expert, const int64_t* __restrict__ indices64, int64_t n, int E,
+    int32_t* __restrict__ route_order, int32_t* __restrict__ expert_offsets, int32_t* __restrict__ active_experts,
+    int32_t* __restrict__ active_count, int64_t* __restrict__ order64, int64_t* __restrict__ offsets64,
+    int tile_tokens, int32_t* __restrict__ tiles, int32_t* __restrict__ tile_count) {
+  constexpr int kChunks = kPermuteMaxRoutes / 64;
+  constexpr int kPer = kChunks / kPermuteWaves;  // chunks per wavefront
+  __shared__ int hist[kChunks][256];
+  __shared__ int cnt[256];
+  __shared__ int start[256];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int nch = static_cast<int>((n + 63) / 64);
+  for (int i = threadIdx.x; i < nch * 256; i += blockDim.x) (&hist[0][0])[i] = 0;
+  __syncthreads();
+
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int ids[kPer], ranks[kPer];
+  bool oks[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int ch = wave + kPermuteWaves * j;
+    oks[j] = false;
+    ids[j] = 0;
+    ranks[j] = 0;
+    if (ch < nch) {  // uniform over the wavefront
+      bool valid;
+      const int id = load_route_id(route_expert, indices64, static_cast<int64_t>(ch) * 64 + lane, n, E, valid);
+      const uint64_t eq = same_id_lanes(id, valid, nbits);
+      ids[j] = id;
+      oks[j] = valid;
+      ranks[j] = __popcll(eq & lt);
+      if (valid && (eq & lt) == 0) hist[ch][id] = __popcll(eq);
+    }
   }
-  if (lane == 0) *active_count = acc;
+  __syncthreads();
+  // per expert: chunk bases (exclusive scan over the chunks) and the total
+  for (int e = threadIdx.x; e < 256; e += blockDim.x) {
+    int run = 0;
+    for (int ch = 0; ch < nch; ++ch) {
+      const int v = hist[ch][e];
+      hist[ch][e] = run;
+      run += v;
+    }
+    cnt[e] = e < E ? run : 0;
+  }
+  __syncthreads();
+  if (wave == 0)
+    expert_tables(cnt, start, lane, E, expert_offsets, offsets64, tile_tokens, tiles, tile_count, active_experts,
+                  active_count);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int ch = wave + kPermuteWaves * j;
+    if (ch < nch && oks[j]) {
+      const int pos = start[ids[j]] + hist[ch][ids[j]] + ranks[j];
+      const int64_t r = static_cast<int64_t>(ch) * 64 + lane;
+      route_order[pos] = static_cast<int32_t>(r);
+      if (order64 != nullptr) order64[pos] = r;
+    }
+  }
 }
 
 hipError_t launch_route_permute(const int32_t* route_expert, const int64_t* indices64, int64_t n_routes,
                                 int64_t E, const RouteTables& rt, int64_t* order64, int64_t* offsets64,
                                 int tile_tokens, hipStream_t stream) {
   if (tile_tokens > 0 && (rt.tiles == nullptr || rt.tile_count == nullptr)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(route_permute_kernel, dim3(1), dim3(64), 0, stream, route_expert, indices64, n_routes,
-                     static_cast<int>(E), rt.route_order, rt.expert_offsets, rt.active_experts, rt.active_count,
-                     order64, offsets64, tile_tokens, rt.tiles, rt.tile_count);
+  if (n_routes > 64 && n_routes <= kPermuteMaxRoutes)
+    hipLaunchKernelGGL(route_permute_wg_kernel, dim3(1), dim3(64 * kPermuteWaves), 0, stream, route_expert, indices64,
+                       n_routes, static_cast<int>(E), rt.route_order, rt.expert_offsets, rt.active_experts,
+                       rt.active_count, order64, offsets64, tile_tokens, rt.tiles, rt.tile_count);
+  else
+    hipLaunchKernelGGL(route_permute_kernel, dim3(1), dim3(64), 0, stream, route_expert, indices64, n_routes,
+                       static_cast<int>(E), rt.route_order, rt.expert_offsets, rt.active_experts, rt.active_count,
+                       order64, offsets64, tile_tokens, rt.tiles, rt.tile_count);
   return hipGetLastError();
 }
 
