@@ -35,10 +35,7 @@
 // 16-byte slots XOR-swizzled by the token index, so the B reads of 16 tokens
 // hit distinct banks.
 //
-// Work tiles come from the device-built tile list (expert, first route); the
-// linear workgroup id is remapped so that each XCD (id % 8) walks a
-// contiguous range of (row block, tile) pairs with tiles fastest: the tiles
-// of one hot expert reuse the same weight rows through that XCD's L2.
+// Work tiles come from the device-built tile list (expert, first route).
 #include <atomic>
 #include <type_traits>
 
@@ -192,11 +189,11 @@ struct MfmaCfg {
   static_assert(D * BUF <= 144 * 1024, "LDS ring too large");
 };
 
-// Persistent workgroups: the (route tile, row block) work items are split into
+// Persistent workgroups: the (row block, route tile) work items are split into
 // 8 contiguous ranges, one per XCD (blockIdx % 8), and each XCD's range into
-// contiguous runs, one per workgroup. Items run row block fastest, so a
-// workgroup walks consecutive row blocks of one tile and the tiles of one hot
-// expert sit side by side in one XCD's range. A workgroup loads the metadata
+// contiguous runs, one per workgroup. Items run tile fastest, so the tiles of
+// one hot expert (or of the shared expert) that share a row block run back to
+// back on one workgroup and re-read its weights from L2. A workgroup loads the metadata
 // of all its items into LDS once; after that its loader waves stream the
 // items' steps back to back through the LDS ring, and the MMA waves write each
 // item's outputs when its last step is done.
@@ -246,7 +243,7 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
   // ---- metadata of the run into LDS (every wave takes part in the barriers) ----
   for (int i = tid; i < nit; i += C::THREADS) {
     const int item = ib + i;
-    const int tile = item / a.row_blocks;
+    const int tile = item % n_tiles;
     int expert = 0, rbeg, nt;
     if (a.tiles != nullptr) {
       expert = a.tiles[2 * tile];
@@ -260,7 +257,7 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
     m[0] = expert;
     m[1] = rbeg;
     m[2] = nt;
-    m[3] = item - tile * a.row_blocks;
+    m[3] = item / n_tiles;
   }
   __syncthreads();
   for (int idx = tid; idx < nit * NTOK; idx += C::THREADS) {
