@@ -19,9 +19,10 @@
  *     allocates device memory or synchronises (except uqm_workspace_status);
  *     temporaries live in the caller's `workspace`, sized by
  *     uqm_moe_workspace_bytes(). The workspace must be zero-filled before its
- *     first use: its first 256 bytes hold synchronisation words that the
- *     single-token fused kernel leaves zero again after every launch. Calls
- *     that overlap in time must not share a workspace.
+ *     first use: its first 4352 bytes hold the single-token fused kernel's
+ *     synchronisation words (an error word and one launch epoch per
+ *     workgroup, advanced by every launch). Calls in order on one stream may
+ *     reuse a workspace; calls that overlap in time must not share one.
  *   - Return 0 on success, nonzero UQM_ERR_* otherwise; the message is in
  *     uqm_last_error() (thread-local). Invalid arguments are rejected before
  *     any launch.
@@ -51,8 +52,8 @@ enum { UQM_Q4 = 0, UQM_Q8 = 1, UQM_BF16 = 2 };
 /* Options for uqm_set_option (process-wide). */
 enum {
   UQM_OPT_FUSED_DECODE = 1,   /* 1 (default): single-token blocks use the fused persistent kernel */
-  UQM_OPT_FUSED_ROUTED_BLOCKS = 2, /* CUs it gives the routed experts when a shared expert is present
-                                      (0, the default: half of the CUs) */
+  UQM_OPT_FUSED_ROUTED_BLOCKS = 2, /* accepted, no effect: every CU of the fused kernel takes a share
+                                      of every phase (values 0..4096 as before) */
   UQM_OPT_MFMA_MIN_TOKENS = 3      /* token count from which multi-token calls run the expert projections
                                       as MFMA grouped GEMMs (default 2; 0 = never, batched GEMV instead) */
 };

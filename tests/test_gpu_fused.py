@@ -82,10 +82,12 @@ def test_repeat_and_grid_size_are_bit_identical(fused_default):
             assert torch.equal(a.view(torch.uint8) if a.dtype == torch.bfloat16 else a,
                                b.view(torch.uint8) if b.dtype == torch.bfloat16 else b)
     hip_ext.workspace_status(ws)
-    sync = ws[: 4 * 8].view(torch.int32).cpu()
-    assert int(sync[1]) == 0, "finished-workgroup counter not reset"
-    assert int(sync[0]) == 5, "the epoch advances once per launch"
-    for nr in (16, 100, 0):
+    # one launch epoch per workgroup (one workgroup per CU), each advanced once per launch
+    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
+    sync = ws[: 4 * (64 + cus)].view(torch.int32).cpu()
+    assert int(sync[4]) == 0, "error word raised"
+    assert torch.equal(sync[64:64 + cus], torch.full((cus,), 5, dtype=torch.int32)), "epochs"
+    for nr in (16, 100, 0):  # the routed-blocks option is accepted and has no effect
         hip_ext.set_option(_native.UQM_OPT_FUSED_ROUTED_BLOCKS, nr)
         other = _block(hip_ext, layer, dense, x, shape, ws)
         assert torch.equal(first[0].view(torch.int16), other[0].view(torch.int16)), f"routed blocks {nr}"

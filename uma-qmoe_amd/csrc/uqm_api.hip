@@ -41,7 +41,7 @@ size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 constexpr int kMaxSplit = 4;
 
 struct Layout {
-  size_t fused_sync, fused_hs, fused_hr, fused_yr, counters, route_expert, route_order, expert_offsets, active_experts,
+  size_t fused_sync, fused_hs, fused_hr, fused_lgt, counters, route_expert, route_order, expert_offsets, active_experts,
       tiles, logits, weights, indices, sg, router_part, h_routed, y_routed, h_shared, y_shared, total;
 };
 
@@ -57,7 +57,7 @@ Layout layout(int64_t T, int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k)
   L.fused_sync = take(4 * uqm::kSyncWords);
   L.fused_hs = take(4 * static_cast<size_t>(Is));
   L.fused_hr = take(4 * static_cast<size_t>(k) * I);
-  L.fused_yr = take(8 * static_cast<size_t>(H));
+  L.fused_lgt = take(8 * static_cast<size_t>(E + 1));
   L.counters = take(256);
   L.route_expert = take(4 * R);
   L.route_order = take(4 * R);
@@ -620,7 +620,7 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
 
   // Single token: one persistent launch for the whole block.
   if (tokens == 1 && g_opt_fused.load(std::memory_order_relaxed) != 0 &&
-      fused_config_id(w->encoding, H, w->intermediate_size, Is, k) >= 0 &&
+      fused_config_id(w->encoding, H, w->intermediate_size, Is, k, E) >= 0 &&
       (w->encoding == UQM_BF16 || (H % w->group_size == 0 && w->intermediate_size % w->group_size == 0))) {
     FusedArgs fa{};
     fa.x = x;
@@ -645,13 +645,12 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
     fa.sync = at<uint32_t>(workspace, L.fused_sync);
     fa.hs = at<uint32_t>(workspace, L.fused_hs);
     fa.hr = at<uint32_t>(workspace, L.fused_hr);
-    fa.yr = at<uint64_t>(workspace, L.fused_yr);
+    fa.lgt = at<uint64_t>(workspace, L.fused_lgt);
     fa.out = static_cast<uint16_t*>(output);
     fa.logits_out = static_cast<uint16_t*>(logits);
     fa.weights_out = static_cast<uint16_t*>(routing_weights);
     fa.indices_out = expert_indices;
-    const int64_t nr = g_opt_fused_routed_blocks.load(std::memory_order_relaxed);
-    return hip_check(launch_moe_decode_fused(w->encoding, fa, static_cast<int>(nr), s), "fused block launch");
+    return hip_check(launch_moe_decode_fused(w->encoding, fa, s), "fused block launch");
   }
 
   // 1-2. router logits (+ shared-gate logit in column E), top-k

@@ -2,41 +2,42 @@
 //
 // A decode step of one MoE block reads ~88 MB of weights (Qwen1.5-MoE shape:
 // 4 routed Q4 experts, the BF16 shared expert, the router) and does almost no
-// arithmetic on them, so its time is HBM time plus every dependent memory
-// round trip of the chain router -> top-k -> routed gate/up -> down that the
-// streaming cannot hide. The reference runs this chain as ~12 launches with
-// host syncs (src/uma_qmoe/native_backend.py:319-372; Transformers router and
-// shared MLP around it, src/uma_qmoe/qwen_compressed_loader.py:67-86).
+// arithmetic on them, so its time is HBM time plus whatever part of the
+// dependent chain router -> top-k -> routed gate/up -> down the streaming
+// cannot hide. The reference runs this chain as ~12 launches with host syncs
+// (src/uma_qmoe/native_backend.py:319-372; Transformers router and shared MLP
+// around it, src/uma_qmoe/qwen_compressed_loader.py:67-86).
 //
-// Here one grid of 8-wave workgroups, one per CU, splits the CUs by role:
+// One workgroup per CU, all resident, each with 8 streaming waves and one
+// control wave. Every CU takes an equal share of every phase:
 //
-//   routed workgroups (the first `routed_blocks`, or all without a shared
-//   expert) each compute the full router from the L2-resident router matrix
-//   (no cross-CU hand-off for routing), run the FP32 softmax / top-k (ties to
-//   the lower expert id) in LDS, then share the routed gate+up rows of the k
-//   selected experts and afterwards the routed down rows, publishing
-//   y_r[o] = sum_k w_k * (down_ek row o . h_k) per output row;
-//   shared workgroups stream the shared expert's gate+up rows, then its down
-//   rows, and write out[o] = bf16(sigmoid(x . w_g) * y_s[o] + y_r[o]).
+//   A  shared gate+up row pairs (no dependence on routing) -> SiLU products;
+//   B  routed gate+up row pairs of the k selected experts -> SiLU products;
+//   C  one or more output rows o: y_s[o] = shared down row o . h_s and
+//      y_r[o] = sum_k w_k * (down_ek row o . h_k), summed in the same wave:
+//      out[o] = bf16(sigmoid(x . w_g) * y_s[o] + y_r[o]).
 //
-// Measured on MI355X: HBM saturates with ~160 CUs streaming, so the shared
-// stream keeps full bandwidth while the latency-bound routed chain runs on
-// CUs whose memory queues hold no bulk traffic ahead of its loads.
+// Routing runs beside phase A: the router rows (plus the shared expert's gate
+// row) are spread over the workgroups, one row each, and published; the
+// control wave of every workgroup polls the published logits, runs the
+// softmax / top-k (ties to the lower expert id) in registers and hands the
+// routes to its streaming waves through LDS. A streaming wave issues its
+// phase-B loads when its phase A is done and the routes are in LDS, together
+// with its phase-C shared down row, and all of its phase-C loads before it
+// waits for the other CUs' SiLU products.
 //
-// Hand-offs between CUs (SiLU products h, y_r) are epoch-tagged words
+// Hand-offs between CUs (router logits, SiLU products) are epoch-tagged words
 // written with agent-scope (sc1) stores, which are coherent across the eight
 // XCD L2 caches. A consumer loads and validates them in one round trip and
 // reloads until every tag carries this launch's epoch; there are no counter
-// barriers and no store drains on the critical path. The epoch is a workspace
-// word that every workgroup reads at start and the last workgroup to finish
-// advances. Every wait is bounded: when a bound expires the kernel raises a
-// sticky error word and still runs to the end, so no wave can hang the device.
-// The waits need all workgroups resident at once: the grid is one 512-thread
-// workgroup per CU.
+// barriers and no store drains on the critical path. Each workgroup keeps its
+// own copy of the epoch in the workspace and advances it once per launch.
+// Every wait is bounded: when a bound expires the kernel raises a sticky error
+// word and still runs to the end, so no wave can hang the device. The waits
+// need all workgroups resident at once: the grid is one workgroup per CU.
 //
-// Within a role, work is split statically and evenly over its waves; each
-// lane streams fixed 16-byte column chunks of every row (non-temporal loads:
-// each weight byte is read once) against activation fragments held in
+// Each lane streams fixed 16-byte column chunks of every row (non-temporal
+// loads: each weight byte is read once) against activation fragments held in
 // registers. Loads are issued branch-free (out-of-row lanes re-read the row's
 // first chunk and are masked in the arithmetic) and all row bookkeeping is
 // wave-uniform, so every load of a batch is in flight before the first wait.
@@ -58,23 +59,15 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 namespace {
 
-// Load batches (rows per wave per round trip). Larger batches mean fewer
-// dependent round trips; smaller ones keep less in flight, which keeps the
-// HBM queue, and so every round trip behind it, short.
-#ifndef UQM_FUSED_ROUTER_RB
-#define UQM_FUSED_ROUTER_RB 8   // router rows
+constexpr int kWaves = 8;                  // streaming waves per workgroup
+constexpr int kThreads = (kWaves + 1) * 64;  // + the control wave
+constexpr int kLdsHeader = 256;            // flags, routes, weights, shared gate (16-byte aligned)
+constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a wait gives up (well over 0.1 s)
+constexpr int kPollSleep = 8;              // s_sleep units (64 clocks) between router logit polls
+constexpr int kRouterHeadStart = 12;       // s_sleep units the streaming waves of router workgroups yield
+#ifndef UQM_FUSED_CTRL_PRIO
+#define UQM_FUSED_CTRL_PRIO 3
 #endif
-#ifndef UQM_FUSED_ROUTED_RB
-#define UQM_FUSED_ROUTED_RB 8   // routed gate+up row pairs
-#endif
-#ifndef UQM_FUSED_SHARED_RB
-#define UQM_FUSED_SHARED_RB 2   // shared gate+up row pairs
-#endif
-
-constexpr int kWaves = 8;                  // waves per workgroup
-constexpr int kThreads = kWaves * 64;
-constexpr int kRoutedLdsHeader = 2576;     // routed-role LDS before the SiLU products (16-byte aligned)
-constexpr uint32_t kSpinLimit = 1u << 20;  // ~0.2 s of polling at s_sleep 8
 
 __device__ __forceinline__ uint4 ld_stream(const uint8_t* p) {
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
@@ -117,44 +110,94 @@ __device__ __forceinline__ uint64_t tag32(uint32_t epoch, float v) {
 // This lane's 16-byte column chunks of a row of C chunks: chunk lane + 64*j,
 // clamped to chunk 0 beyond the row (the load stays inside the row and is
 // coalesced with lane 0's), with a 0/1 mask and the offset of its scale.
+// Chunk and mask are recomputed at each use (two VALU ops) rather than held
+// in registers; scale offsets (a division) are kept for scaled encodings.
 template <int ENC, int CPL>
 struct Cols {
-  int c[CPL];
-  int s[CPL];
-  float m[CPL];
+  int C, ln;
+  int sc[Enc<ENC>::kScaled ? CPL : 1];
+  __device__ __forceinline__ int c(int j) const {
+    const int v = ln + 64 * j;
+    return v < C ? v : 0;
+  }
+  __device__ __forceinline__ float m(int j) const { return ln + 64 * j < C ? 1.f : 0.f; }
+  __device__ __forceinline__ int s(int j) const {
+    if constexpr (Enc<ENC>::kScaled) return sc[j];
+    return 0;
+  }
 };
 
+// Lane id the compiler cannot merge with threadIdx-derived values: column
+// offsets built from it for a rarely taken loop are recomputed there instead
+// of being kept live (in registers) from the first use.
+__device__ __forceinline__ int opaque_lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// A zero the compiler treats as per-lane: a load from `p + opaque_zero()` is
+// not copied to a scalar register right after issue, so the wave waits for it
+// only where the value is used.
+__device__ __forceinline__ int opaque_zero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
+// Returns v, but only once `dep` has been computed: keeps the compiler from
+// hoisting a use of a loaded value (and the wait for its load) above `dep`.
+__device__ __forceinline__ uint32_t pinned_after(uint32_t v, float dep) {
+  asm volatile("" : "+v"(v) : "v"(dep));
+  return v;
+}
+
 template <int ENC, int CPL>
-__device__ __forceinline__ void make_cols(int C, int group, Cols<ENC, CPL>& cl) {
-  const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void make_cols(int C, int group, Cols<ENC, CPL>& cl, int ln = -1) {
+  cl.C = C;
+  cl.ln = ln >= 0 ? ln : static_cast<int>(threadIdx.x & 63);
+  if constexpr (Enc<ENC>::kScaled) {
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const int c = lane + 64 * j;
-    const bool ok = c < C;
-    cl.c[j] = ok ? c : 0;
-    cl.m[j] = ok ? 1.f : 0.f;
-    cl.s[j] = Enc<ENC>::kScaled ? (cl.c[j] * Enc<ENC>::kElems) / group : 0;
+    for (int j = 0; j < CPL; ++j) cl.sc[j] = (cl.c(j) * Enc<ENC>::kElems) / group;
   }
 }
 
-// Fragments of a BF16 activation row (global or LDS) for this lane's chunks.
+// A BF16 activation row's raw words at this lane's chunks (global or LDS),
+// and the fragments built from them. Split so that a wave can issue the raw
+// loads early and build the fragments after issuing its weight loads.
 template <int ENC, int CPL>
-__device__ __forceinline__ void frags_from(const uint16_t* row, const Cols<ENC, CPL>& cl, XFrag<ENC> (&f)[CPL]) {
+struct XRaw {
+  uint32_t w[CPL][Enc<ENC>::kElems / 2];
+};
+
+template <int ENC, int CPL>
+__device__ __forceinline__ void load_x(const uint16_t* row, const Cols<ENC, CPL>& cl, XRaw<ENC, CPL>& r) {
   using E = Enc<ENC>;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const uint16_t* src = row + static_cast<int64_t>(cl.c[j]) * E::kElems;
-    uint32_t raw[E::kElems / 2];
+    const uint16_t* src = row + static_cast<uint32_t>(cl.c(j) * E::kElems);
 #pragma unroll
     for (int q = 0; q < E::kElems / 8; ++q) {
       const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * q);
-      raw[4 * q] = v.x;
-      raw[4 * q + 1] = v.y;
-      raw[4 * q + 2] = v.z;
-      raw[4 * q + 3] = v.w;
+      r.w[j][4 * q] = v.x;
+      r.w[j][4 * q + 1] = v.y;
+      r.w[j][4 * q + 2] = v.z;
+      r.w[j][4 * q + 3] = v.w;
     }
-    make_frag<ENC>(raw, f[j]);
   }
+}
+
+template <int ENC, int CPL>
+__device__ __forceinline__ void frags_of(const XRaw<ENC, CPL>& r, XFrag<ENC> (&f)[CPL]) {
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) make_frag<ENC>(r.w[j], f[j]);
+}
+
+template <int ENC, int CPL>
+__device__ __forceinline__ void frags_from(const uint16_t* row, const Cols<ENC, CPL>& cl, XFrag<ENC> (&f)[CPL]) {
+  XRaw<ENC, CPL> r;
+  load_x<ENC, CPL>(row, cl, r);
+  frags_of<ENC, CPL>(r, f);
 }
 
 // One matrix row's 16-byte chunks at this lane's columns, plus their scales.
@@ -170,8 +213,9 @@ __device__ __forceinline__ void issue_row(const uint8_t* row, const float* srow,
                                           RowLoad<ENC, CPL>& r) {
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    r.w[j] = ld_stream(row + static_cast<int64_t>(cl.c[j]) * 16);
-    if constexpr (Enc<ENC>::kScaled) r.s[j] = ld_stream(srow + cl.s[j]);
+    // 32-bit lane offsets from a uniform row address (the SGPR-base form)
+    r.w[j] = ld_stream(row + static_cast<uint32_t>(cl.c(j) * 16));
+    if constexpr (Enc<ENC>::kScaled) r.s[j] = ld_stream(srow + static_cast<uint32_t>(cl.s(j)));
   }
 }
 
@@ -182,7 +226,7 @@ __device__ __forceinline__ float dot_row(const RowLoad<ENC, CPL>& r, const XFrag
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const float d = dot_chunk<ENC>(r.w[j], f[j]);
-    acc = fmaf(d, Enc<ENC>::kScaled ? r.s[j] * cl.m[j] : cl.m[j], acc);
+    acc = fmaf(d, Enc<ENC>::kScaled ? r.s[j] * cl.m(j) : cl.m(j), acc);
   }
   return acc;
 }
@@ -192,30 +236,57 @@ __device__ __forceinline__ float lane_value(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Workgroup-cooperative copy of n epoch-tagged bf16 words into LDS. Reloads
-// until every tag equals `epoch` (the producers' sc1 stores have landed).
-__device__ void stage_tagged16(const uint32_t* src, int n, uint16_t* dst, uint32_t epoch, uint32_t* error) {
-  const uint64_t* s64 = reinterpret_cast<const uint64_t*>(src);
-  uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
-  const int n2 = n / 2;
-  for (uint32_t spins = 0;; ++spins) {
-    int ok = 1;
-    for (int i = threadIdx.x; i < n2; i += kThreads) {
-      const uint64_t v = co_load(s64 + i);
-      const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
-      ok &= (lo >> 16) == epoch && (hi >> 16) == epoch;
-      d32[i] = (lo & 0xFFFFu) | (hi << 16);
-    }
-    if (__syncthreads_and(ok)) return;
-    if (spins > kSpinLimit) {
-      if (threadIdx.x == 0) atomicOr(error, 1u);
-      return;
-    }
-    __builtin_amdgcn_s_sleep(8);
-  }
+// Bare workgroup barrier: completes this wave's LDS operations first, but
+// leaves its outstanding global loads in flight (a streaming wave can hold a
+// whole batch of weight rows across it).
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#define UQM_MAXSTEP(O) v = max(v, static_cast<uint32_t>(__float_as_int(xor_partner<O>(__int_as_float(static_cast<int>(v))))))
+  UQM_MAXSTEP(32);
+  UQM_MAXSTEP(16);
+  UQM_MAXSTEP(8);
+  UQM_MAXSTEP(4);
+  UQM_MAXSTEP(2);
+  UQM_MAXSTEP(1);
+#undef UQM_MAXSTEP
+  return v;
+}
+
+// Order-preserving 16-bit key of a bf16 value: larger value, larger key; -0
+// and +0 share a key; NaN sorts above +inf (as a descending torch.sort puts
+// it first). Keys of non-NaN values are >= 0x007F, so 0 marks "taken".
+__device__ __forceinline__ uint32_t bf16_key(uint16_t u) {
+  if ((u & 0x7FFFu) > 0x7F80u) return 0xFFFFu;
+  if (u == 0x8000u) u = 0;
+  return (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
+}
+__device__ __forceinline__ float bf16_of_key(uint32_t key) {
+  const uint32_t u = (key & 0x8000u) ? (key & 0x7FFFu) : (~key & 0xFFFFu);
+  return bf16_to_f32(static_cast<uint16_t>(u));
+}
+
+// [lo, hi) of n items split evenly over `parts`.
+// (part * n must fit in 32 bits: parts <= 8192 waves, n <= 2^18.)
+__device__ __forceinline__ int split_at(int n, int part, int parts) {
+  return uniform(static_cast<int>(static_cast<uint32_t>(part) * static_cast<uint32_t>(n) / static_cast<uint32_t>(parts)));
 }
 
 }  // namespace
+
+// LDS of one workgroup: header | shared SiLU products [Is] bf16 | routed SiLU
+// products [k, I] bf16 | routed fragments [k * CR][kXWords] u32 | their offset
+// terms [k * CR] f32, where CR = I / elems is the chunk count of a routed row.
+template <int ENC>
+size_t fused_lds_bytes(int64_t I, int64_t Is, int64_t k) {
+  const int64_t jobs = k * (I / Enc<ENC>::kElems);
+  return kLdsHeader + 2 * static_cast<size_t>(Is + k * I) + static_cast<size_t>(jobs) * (4 * Enc<ENC>::kXWords + 4);
+}
 
 // Template parameters: routed encoding; 16-byte chunks per lane for a BF16
 // row of H (CH), an encoded row of H (CHR), an encoded row of I (CIR) and a
@@ -225,24 +296,52 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   using ER = Enc<ENC>;
   constexpr int CISX = CIS > 0 ? CIS : 1;  // array extent when there is no shared expert
   constexpr bool kShared = CIS > 0;
+  // Routed gate+up row pairs per load batch (the most a wave takes at the
+  // shapes served: 5632 pairs / 2048 waves with a shared expert, 8192 / 2048
+  // without), and their value count rounded up to a power of two.
+  constexpr int RBP = CHR == 1 ? (kShared ? 3 : 4) : (CHR == 2 ? 2 : 1);
+  constexpr int VB = RBP == 3 ? 8 : 2 * RBP;
+  // Routed down chunks per lane: the k rows of an output row are flattened
+  // over the wave's lanes (k * CR chunks).
+  constexpr int NJ = KMAX * CIR;
+  // 64-bit tag loads per lane per staging round (fewer when many routed down
+  // chunks are held in registers)
+  constexpr int SL = NJ > 4 ? 4 : 12;
+  constexpr int LPL = 5;  // router logits per lane: E + 1 <= 320
   extern __shared__ __align__(16) unsigned char lds[];
+  const int H = static_cast<int>(a.H), I = static_cast<int>(a.I), Is = kShared ? static_cast<int>(a.Is) : 0;
+  const int E = a.E, k = a.k;
+  const int CR = I / ER::kElems;  // chunks per routed down row
+  const int jobs = k * CR;
+  int* l_route = reinterpret_cast<int*>(lds);
+  float* l_w = reinterpret_cast<float*>(lds + 32);
+  float* l_sg = reinterpret_cast<float*>(lds + 64);
+  uint16_t* lhs = reinterpret_cast<uint16_t*>(lds + kLdsHeader);
+  uint16_t* lhr = lhs + Is;
+  uint32_t* lfr = reinterpret_cast<uint32_t*>(lds + kLdsHeader + 2 * (Is + k * I));
+  float* loff = reinterpret_cast<float*>(lfr + jobs * ER::kXWords);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nb = static_cast<int>(gridDim.x);
   const int b = static_cast<int>(blockIdx.x);
-  const int gw = b * kWaves + wave;  // for trace hooks
+  const int gw = b * (kWaves + 1) + wave;  // for trace hooks
   (void)gw;
   UQM_FUSED_TRACE_INIT
-  const int H = static_cast<int>(a.H), I = static_cast<int>(a.I), Is = static_cast<int>(a.Is);
-  const int E = a.E, k = a.k;
-  uint32_t* const sync = a.sync;
+  UQM_FUSED_TRACE(0);
   uint32_t* const error = a.sync + kSyncError;
+  uint32_t* const my_epoch = a.sync + kSyncEpochBase + b;
   const int group = ER::kScaled ? a.group : 1;
-  const int nr = kShared ? a.routed_blocks : nb;  // routed workgroups
+  const int nrow = E + (kShared ? 1 : 0);  // router rows + the shared-expert gate row
 
-  uint32_t epoch = (co_load(sync + kSyncEpoch) + 1u) & 0xFFFFu;
-  if (epoch == 0) epoch = 1;  // tag 0 never marks valid data (zero-filled workspace)
-  epoch = static_cast<uint32_t>(uniform(static_cast<int>(epoch)));
+  // Every workgroup keeps its own copy of the launch epoch and advances it
+  // once per launch, so all copies agree without any cross-workgroup atomic.
+  // Tag 0 never marks valid data (zero-filled workspace).
+  // (Kept per lane, not made uniform: a uniform copy would make the wave
+  // wait for the load at the copy.)
+  auto next_epoch = [](uint32_t last) {
+    const uint32_t e = (last + 1u) & 0xFFFFu;
+    return e == 0 ? 1u : e;
+  };
 
   const int64_t rowH16 = static_cast<int64_t>(H) * 2, rowHR = static_cast<int64_t>(H) * ER::kBitsPerWeight / 8,
                 rowIR = static_cast<int64_t>(I) * ER::kBitsPerWeight / 8, rowIS = static_cast<int64_t>(Is) * 2;
@@ -250,313 +349,423 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
 
   Cols<kBF16, CH> colH16;
   make_cols<kBF16, CH>(H / 8, 1, colH16);
-  XFrag<kBF16> xb[CH];
-  frags_from<kBF16, CH>(a.x, colH16, xb);
-  UQM_FUSED_TRACE(0);
 
-  if (b < nr) {
-    // =========================================================== routed role
-    // LDS: logits [256] f32 | ranks [256] i32 | slots [64] i32 | slot weights [64] f32 |
-    //      softmax max, sum | routed SiLU products [k, I] bf16
-    float* lg = reinterpret_cast<float*>(lds);
-    int* lrank = reinterpret_cast<int*>(lds + 1024);
-    int* lslot = reinterpret_cast<int*>(lds + 2048);
-    float* lsw = reinterpret_cast<float*>(lds + 2304);
-    float* lstat = reinterpret_cast<float*>(lds + 2560);
-    uint16_t* lhr = reinterpret_cast<uint16_t*>(lds + kRoutedLdsHeader);
-    const int wr = nr * kWaves;      // routed waves
-    const int rw = b * kWaves + wave;
-
-    // Router: this workgroup computes every logit (the router rows come from
-    // L2 after the first workgroup of each XCD has read them).
-    constexpr int RBR = UQM_FUSED_ROUTER_RB;
-    for (int r0 = wave * RBR; r0 < E; r0 += kWaves * RBR) {
-      RowLoad<kBF16, CH> rl[RBR];
+  // Builds the routed fragments (once per workgroup, from the staged routed
+  // products): every wave takes part, between the staging and the final
+  // barrier.
+  auto build_fragments = [&]() {
+    for (int jb = threadIdx.x; jb < jobs; jb += kThreads) {
+      const int s = jb / CR, c = jb - s * CR;
+      const uint16_t* src = lhr + s * I + c * ER::kElems;
+      uint32_t raw[ER::kElems / 2];
 #pragma unroll
-      for (int q = 0; q < RBR; ++q) {
-        const int r = r0 + q < E ? r0 + q : r0;
-        issue_row<kBF16, CH>(a.router + r * rowH16, nullptr, colH16, rl[q]);
+      for (int q = 0; q < ER::kElems / 8; ++q) {
+        const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * q);
+        raw[4 * q] = v.x;
+        raw[4 * q + 1] = v.y;
+        raw[4 * q + 2] = v.z;
+        raw[4 * q + 3] = v.w;
       }
-      float v[RBR];
+      XFrag<ENC> f;
+      make_frag<ENC>(raw, f);
 #pragma unroll
-      for (int q = 0; q < RBR; ++q) v[q] = dot_row<kBF16, CH>(rl[q], xb, colH16);
-      const float sum = wave_multi_sum<RBR>(v);
-      const int q = lane >> (6 - log2_of<RBR>());
-      if ((lane & ((64 / RBR) - 1)) == 0 && r0 + q < E) lg[r0 + q] = round_bf16(sum);
+      for (int q = 0; q < ER::kXWords / 4; ++q)
+        *reinterpret_cast<uint4*>(lfr + jb * ER::kXWords + 4 * q) =
+            make_uint4(f.w[4 * q], f.w[4 * q + 1], f.w[4 * q + 2], f.w[4 * q + 3]);
+      loff[jb] = f.off;
     }
-    if (threadIdx.x < 256) lrank[threadIdx.x] = 0;
-    if (threadIdx.x < 64) {
-      lslot[threadIdx.x] = 0;  // defined even if NaN logits leave a rank unused
-      lsw[threadIdx.x] = 0.f;
-    }
-    __syncthreads();
+  };
 
-    // Top-k by ranking, spread over the workgroup: rank(e) = #larger logits
-    // + #equal logits with a lower id (ties go to the lower expert id). Item
-    // (e, c) counts over the c-th eighth of the logits.
-    for (int it = threadIdx.x; it < E * 8; it += kThreads) {
-      const int e = it % E, c = it / E;
-      const float le = lg[e];
-      int cnt = 0;
-      for (int j = c * E / 8; j < (c + 1) * E / 8; ++j) {
-        const float lj = lg[j];
-        cnt += static_cast<int>(lj > le) | (static_cast<int>(lj == le) & static_cast<int>(j < e));
-      }
-      if (cnt) atomicAdd(&lrank[e], cnt);
+  if (wave == kWaves) {
+    // ========================================================= control wave
+    // Routing is on every wave's critical path: its instructions go first
+    // when it shares a SIMD with streaming waves.
+    __builtin_amdgcn_s_setprio(UQM_FUSED_CTRL_PRIO);
+    // Activation, epoch and router row loads go out together: one round trip.
+    XRaw<kBF16, CH> x_raw;
+    load_x<kBF16, CH>(a.x, colH16, x_raw);
+    const uint32_t last_epoch = co_load(my_epoch + opaque_zero());
+    for (int r = b; r < nrow; r += nb) {
+      RowLoad<kBF16, CH> rl;
+      issue_row<kBF16, CH>(r < E ? a.router + r * rowH16 : a.shared_expert_gate, nullptr, colH16, rl);
+      XFrag<kBF16> xb[CH];
+      frags_of<kBF16, CH>(x_raw, xb);
+      const float g = wave_sum(dot_row<kBF16, CH>(rl, xb, colH16));
+      if (lane == 0) co_store<uint64_t>(a.lgt + r, tag32(next_epoch(pinned_after(last_epoch, g)), round_bf16(g)));
     }
-    if (wave == 0) {  // FP32 softmax statistics
-      float mx = -INFINITY;
-      for (int e = lane; e < E; e += 64) mx = fmaxf(mx, lg[e]);
-      mx = wave_max(mx);
-      float se = 0.f;
-      for (int e = lane; e < E; e += 64) se += __expf(lg[e] - mx);
-      se = wave_sum(se);
-      if (lane == 0) {
-        lstat[0] = mx;
-        lstat[1] = se;
+    const uint32_t epoch = next_epoch(last_epoch);
+    UQM_FUSED_TRACE(1);
+    // Every logit, once all its producers have published it. Three polls are
+    // kept in flight, a short sleep apart, so a late producer is seen one
+    // spacing (not one round trip) after it publishes; every poll issues the
+    // same loads (lanes past the end re-read the last word), which keeps the
+    // compiler's waits for the oldest poll exact.
+    uint64_t pa[LPL], pb[LPL], pc[LPL];
+    auto poll = [&](uint64_t (&t)[LPL]) {
+#pragma unroll
+      for (int j = 0; j < LPL; ++j) t[j] = co_load(a.lgt + min(lane + 64 * j, nrow - 1));
+    };
+    auto ready = [&](const uint64_t (&t)[LPL]) {
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < LPL; ++j) ok &= static_cast<uint32_t>(t[j] >> 32) == epoch || lane + 64 * j >= nrow;
+      return __all(ok) != 0;
+    };
+    float lv[LPL];
+    auto take = [&](const uint64_t (&t)[LPL]) {
+#pragma unroll
+      for (int j = 0; j < LPL; ++j) lv[j] = __uint_as_float(static_cast<uint32_t>(t[j]));
+    };
+    poll(pa);
+    __builtin_amdgcn_s_sleep(kPollSleep);
+    poll(pb);
+    __builtin_amdgcn_s_sleep(kPollSleep);
+    poll(pc);
+    for (uint32_t round = 0;; ++round) {
+      if (ready(pa)) {
+        take(pa);
+        break;
+      }
+      if (round > kSpinLimit / 4) {
+        if (lane == 0) atomicOr(error, 1u);
+        take(pa);
+        break;
+      }
+      poll(pa);
+      __builtin_amdgcn_s_sleep(kPollSleep);
+      if (ready(pb)) {
+        take(pb);
+        break;
+      }
+      poll(pb);
+      __builtin_amdgcn_s_sleep(kPollSleep);
+      if (ready(pc)) {
+        take(pc);
+        break;
+      }
+      poll(pc);
+      __builtin_amdgcn_s_sleep(kPollSleep);
+    }
+    UQM_FUSED_TRACE(2);
+    // FP32 softmax statistics over the E expert logits.
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < LPL; ++j)
+      if (lane + 64 * j < E) mx = fmaxf(mx, lv[j]);
+    mx = wave_max(mx);
+    float se = 0.f;
+#pragma unroll
+    for (int j = 0; j < LPL; ++j)
+      if (lane + 64 * j < E) se += __expf(lv[j] - mx);
+    se = wave_sum(se);
+    // Top-k by k rounds of a wave max over (value key, 0xFFFF - id): the
+    // largest logit wins, equal logits go to the lower expert id.
+    uint32_t key[LPL];
+#pragma unroll
+    for (int j = 0; j < LPL; ++j) {
+      const int e = lane + 64 * j;
+      key[j] = e < E ? (bf16_key(f32_to_bf16(lv[j])) << 16) | static_cast<uint32_t>(0xFFFF - e) : 0u;
+    }
+    int route_e = 0;
+    float route_l = 0.f;
+    for (int s = 0; s < k; ++s) {
+      uint32_t m = key[0];
+#pragma unroll
+      for (int j = 1; j < LPL; ++j) m = max(m, key[j]);
+      m = wave_max_u32(m);
+#pragma unroll
+      for (int j = 0; j < LPL; ++j)
+        if (key[j] == m) key[j] = 0u;
+      if (lane == s) {
+        route_e = 0xFFFF - static_cast<int>(m & 0xFFFFu);
+        route_l = bf16_of_key(m >> 16);
       }
     }
-    __syncthreads();
-    for (int e = threadIdx.x; e < E; e += kThreads) {
-      const int r = lrank[e];
-      if (r < k) {
-        lslot[r] = e;
-        lsw[r] = __expf(lg[e] - lstat[0]) / lstat[1];
-      }
-    }
-    __syncthreads();
-    const int route_e = lane < k ? lslot[lane] : 0;
-    float p = lane < k ? lsw[lane] : 0.f;
+    float p = lane < k ? __expf(route_l - mx) / se : 0.f;
     if (a.norm) p = p / wave_sum(p);
     const uint16_t wb = f32_to_bf16(p);
-    const float route_w = lane < k ? bf16_to_f32(wb) : 0.f;
-    if (b == 0 && wave == 0) {
+    if (lane < k) {
+      l_route[lane] = route_e;
+      l_w[lane] = bf16_to_f32(wb);
+    }
+    if constexpr (kShared) {
+      float le = 0.f;
+#pragma unroll
+      for (int j = 0; j < LPL; ++j)
+        if (j == (E >> 6)) le = lv[j];
+      const float gl = lane_value(le, E & 63);
+      if (lane == 0) *l_sg = round_bf16(sigmoidf_(gl));
+    }
+    if (b == 0) {
       if (lane < k) {
         if (a.weights_out != nullptr) a.weights_out[lane] = wb;
         if (a.indices_out != nullptr) a.indices_out[lane] = route_e;
       }
-      if (a.logits_out != nullptr)
-        for (int e = lane; e < E; e += 64) a.logits_out[e] = f32_to_bf16(lg[e]);
-    }
-    UQM_FUSED_TRACE(1);
-
-    // Routed gate+up rows q = slot * I + i, split over the routed waves.
-    {
-      Cols<ENC, CHR> colHR;
-      make_cols<ENC, CHR>(H / ER::kElems, group, colHR);
-      XFrag<ENC> xr[CHR];
-      frags_from<ENC, CHR>(a.x, colHR, xr);
-      const int64_t spe = static_cast<int64_t>(I) * hpg;  // gate/up scales per expert
-      const int nq = k * I;
-      const int qa = uniform(static_cast<int>(static_cast<int64_t>(rw) * nq / wr));
-      const int qb = uniform(static_cast<int>(static_cast<int64_t>(rw + 1) * nq / wr));
-      constexpr int RB = UQM_FUSED_ROUTED_RB;
-      int slot = qa / I;
-      int row = qa - slot * I;
-      for (int q0 = qa; q0 < qb; q0 += RB) {
-        const int n = qb - q0 < RB ? qb - q0 : RB;
-        RowLoad<ENC, CHR> rl[RB][2];
-        const int first_slot = slot, first_row = row;
+      if (a.logits_out != nullptr) {
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          const int sl = rb < n ? slot : first_slot;  // rows past the range re-read the first row
-          const int i = rb < n ? row : first_row;
-          const int64_t e = lane_value(route_e, sl);
-          const int64_t grow = e * I + i;
-          issue_row<ENC, CHR>(a.eg + grow * rowHR, a.egs + e * spe + static_cast<int64_t>(i) * hpg, colHR, rl[rb][0]);
-          issue_row<ENC, CHR>(a.eu + grow * rowHR, a.eus + e * spe + static_cast<int64_t>(i) * hpg, colHR, rl[rb][1]);
-          if (rb < n && ++row == I) {
-            row = 0;
-            ++slot;
-          }
-        }
-        constexpr int V = 2 * RB;
-        float v[V];
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          v[2 * rb] = dot_row<ENC, CHR>(rl[rb][0], xr, colHR);
-          v[2 * rb + 1] = dot_row<ENC, CHR>(rl[rb][1], xr, colHR);
-        }
-        const float sum = wave_multi_sum<V>(v);
-        constexpr int kL = log2_of<V>();
-        const float partner = xor_partner<64 / V>(sum);
-        const int idx = lane >> (6 - kL);
-        const bool writer = (lane & ((64 >> kL) - 1)) == 0 && (idx & 1) == 0;
-        const int rb = idx >> 1;
-        if (writer && rb < n)
-          co_store<uint32_t>(a.hr + q0 + rb, tag16(epoch, f32_to_bf16(silu(round_bf16(sum)) * round_bf16(partner))));
+        for (int j = 0; j < LPL; ++j)
+          if (lane + 64 * j < E) a.logits_out[lane + 64 * j] = f32_to_bf16(lv[j]);
       }
     }
-    UQM_FUSED_TRACE(2);
-
-    // Routed down rows: y_r[o] = sum_s w_s * (down_{e_s} row o . h_s).
-    {
-      Cols<ENC, CIR> colIR;
-      make_cols<ENC, CIR>(I / ER::kElems, group, colIR);
-      const int64_t spd = static_cast<int64_t>(H) * ipg;  // down scales per expert
-      const int oa = uniform(static_cast<int>(static_cast<int64_t>(rw) * H / wr));
-      const int ob = uniform(static_cast<int>(static_cast<int64_t>(rw + 1) * H / wr));
-      // rows per batch: about 32 chunk loads per lane in flight
-      constexpr int RB = KMAX * CIR <= 8 ? 4 : (KMAX * CIR <= 16 ? 2 : 1);
-      RowLoad<ENC, CIR> rr[RB][KMAX];
-      auto issue_rows = [&](int o0, int n) {
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          const int o = rb < n ? o0 + rb : o0;
-#pragma unroll
-          for (int s = 0; s < KMAX; ++s) {
-            if (s < k) {
-              const int64_t e = lane_value(route_e, s);
-              issue_row<ENC, CIR>(a.ed + (e * H + o) * rowIR, a.eds + e * spd + static_cast<int64_t>(o) * ipg,
-                                  colIR, rr[rb][s]);
-            }
-          }
-        }
-      };
-      if (oa < ob) issue_rows(oa, ob - oa < RB ? ob - oa : RB);
-      UQM_FUSED_TRACE(3);
-      stage_tagged16(a.hr, k * I, lhr, epoch, error);
-      UQM_FUSED_TRACE(4);
-      for (int o0 = oa; o0 < ob; o0 += RB) {
-        const int n = ob - o0 < RB ? ob - o0 : RB;
-        if (o0 > oa) issue_rows(o0, n);
-        float y[RB];
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) y[rb] = 0.f;
-#pragma unroll
-        for (int s = 0; s < KMAX; ++s) {
-          if (s < k) {
-            XFrag<ENC> fr[CIR];
-            frags_from<ENC, CIR>(lhr + s * I, colIR, fr);
-            float v[RB];
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) v[rb] = dot_row<ENC, CIR>(rr[rb][s], fr, colIR);
-            const float sum = wave_multi_sum<RB>(v);
-            const float w = lane_value(route_w, s);
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) y[rb] = fmaf(w, lane_value(sum, rb * (64 / RB)), y[rb]);
-          }
-        }
-        if (lane < n) {
-          float yo = y[0];
-#pragma unroll
-          for (int rb = 1; rb < RB; ++rb)
-            if (lane == rb) yo = y[rb];
-          if constexpr (kShared)
-            co_store<uint64_t>(a.yr + o0 + lane, tag32(epoch, yo));
-          else
-            a.out[o0 + lane] = f32_to_bf16(yo);
-        }
-      }
-    }
-    UQM_FUSED_TRACE(5);
-  } else if constexpr (kShared) {
-    // =========================================================== shared role
-    uint16_t* lhs = reinterpret_cast<uint16_t*>(lds);  // [Is] shared SiLU product
-    float* lsg = reinterpret_cast<float*>(lds + ((2 * static_cast<size_t>(Is) + 15) & ~static_cast<size_t>(15)));
-    const int ws = (nb - nr) * kWaves;  // shared waves
-    const int sw = (b - nr) * kWaves + wave;
-
-    // Shared gate+up rows, two row pairs per load batch.
-    {
-      const int pa = uniform(static_cast<int>(static_cast<int64_t>(sw) * Is / ws));
-      const int pb = uniform(static_cast<int>(static_cast<int64_t>(sw + 1) * Is / ws));
-      constexpr int RB = UQM_FUSED_SHARED_RB;
-      for (int r0 = pa; r0 < pb; r0 += RB) {
-        const int n = pb - r0 < RB ? pb - r0 : RB;
-        RowLoad<kBF16, CH> rl[RB][2];
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          const int64_t r = rb < n ? r0 + rb : r0;  // rows past the range re-read row r0
-          issue_row<kBF16, CH>(a.sg_w + r * rowH16, nullptr, colH16, rl[rb][0]);
-          issue_row<kBF16, CH>(a.su_w + r * rowH16, nullptr, colH16, rl[rb][1]);
-        }
-        constexpr int V = 2 * RB;
-        float v[V];
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          v[2 * rb] = dot_row<kBF16, CH>(rl[rb][0], xb, colH16);
-          v[2 * rb + 1] = dot_row<kBF16, CH>(rl[rb][1], xb, colH16);
-        }
-        const float sum = wave_multi_sum<V>(v);
-        constexpr int kL = log2_of<V>();
-        const float partner = xor_partner<64 / V>(sum);
-        const int idx = lane >> (6 - kL);
-        const bool writer = (lane & ((64 >> kL) - 1)) == 0 && (idx & 1) == 0;
-        const int rb = idx >> 1;
-        if (writer && rb < n)
-          co_store<uint32_t>(a.hs + r0 + rb, tag16(epoch, f32_to_bf16(silu(round_bf16(sum)) * round_bf16(partner))));
-      }
-    }
-    // Sigmoid of the shared-expert gate logit (one row, from L2).
-    if (wave == 0) {
-      RowLoad<kBF16, CH> rl;
-      issue_row<kBF16, CH>(a.shared_expert_gate, nullptr, colH16, rl);
-      const float g = wave_sum(dot_row<kBF16, CH>(rl, xb, colH16));
-      if (lane == 0) *lsg = round_bf16(sigmoidf_(round_bf16(g)));
-    }
-    UQM_FUSED_TRACE(2);
-
-    // Shared down rows and the combine with y_r.
-    {
-      Cols<kBF16, CISX> colIS;
-      make_cols<kBF16, CISX>(Is / 8, 1, colIS);
-      const int oa = uniform(static_cast<int>(static_cast<int64_t>(sw) * H / ws));
-      const int ob = uniform(static_cast<int>(static_cast<int64_t>(sw + 1) * H / ws));
-      RowLoad<kBF16, CISX> rs;
-      if (oa < ob) issue_row<kBF16, CISX>(a.sd_w + oa * rowIS, nullptr, colIS, rs);
-      UQM_FUSED_TRACE(3);
-      stage_tagged16(a.hs, Is, lhs, epoch, error);
-      UQM_FUSED_TRACE(4);
-      const float sg = *lsg;
-      for (int o = oa; o < ob; ++o) {
-        if (o > oa) issue_row<kBF16, CISX>(a.sd_w + o * rowIS, nullptr, colIS, rs);
-        XFrag<kBF16> fs[CISX];
-        frags_from<kBF16, CISX>(lhs, colIS, fs);
-        const float ys = wave_sum(dot_row<kBF16, CISX>(rs, fs, colIS));
-        if (lane == 0) {
-          uint64_t t = co_load(a.yr + o);
-          for (uint32_t spins = 0; static_cast<uint32_t>(t >> 32) != epoch; ++spins) {
-            if (spins > kSpinLimit) {
-              atomicOr(error, 1u);
-              break;
-            }
-            __builtin_amdgcn_s_sleep(8);
-            t = co_load(a.yr + o);
-          }
-          a.out[o] = f32_to_bf16(fmaf(sg, ys, __uint_as_float(static_cast<uint32_t>(t))));
-        }
-      }
-    }
-    UQM_FUSED_TRACE(5);
+    UQM_FUSED_TRACE(3);
+    lds_barrier();  // routes ready
+    lds_barrier();  // SiLU products staged
+    build_fragments();
+    lds_barrier();  // routed fragments built
+    if (lane == 0) co_store<uint32_t>(my_epoch, epoch);
+    return;
   }
 
-  // ---------------------------------------------------------------- finish
-  drain();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t old = atomicAdd(sync + kSyncBlocksDone, 1u);
-    if (old == static_cast<uint32_t>(nb - 1)) {
-      co_store<uint32_t>(sync + kSyncEpoch, epoch);
-      co_store<uint32_t>(sync + kSyncBlocksDone, 0u);
+  // ======================================================= streaming waves
+  // In the workgroups that compute a router row, the streaming waves let the
+  // control wave's loads go first, so that routing is not queued behind them.
+  if (b < nrow) __builtin_amdgcn_s_sleep(kRouterHeadStart);
+  const int sw = b * kWaves + wave, nsw = nb * kWaves;
+  Cols<ENC, CHR> colHR;
+  make_cols<ENC, CHR>(H / ER::kElems, group, colHR);
+  const int64_t spe = static_cast<int64_t>(I) * hpg;  // gate/up scales per expert
+  const int64_t spd = static_cast<int64_t>(H) * ipg;  // down scales per expert
+
+  // Activation words and the epoch first: waits for them then never wait for
+  // weight rows issued later.
+  XRaw<kBF16, CH> xb_raw;
+  if constexpr (kShared) load_x<kBF16, CH>(a.x, colH16, xb_raw);
+  XRaw<ENC, CHR> xr_raw;
+  load_x<ENC, CHR>(a.x, colHR, xr_raw);
+  const uint32_t last_epoch = co_load(my_epoch + opaque_zero());
+  // The epoch is derived from last_epoch where each product is stored, after
+  // that product's dot (see pinned_after).
+  auto epoch_after = [&](float dep) { return next_epoch(pinned_after(last_epoch, dep)); };
+
+  // Phase A: shared gate+up row pairs, one pair in flight per wave (64 KB per
+  // CU: enough to keep HBM busy, shallow enough that the control wave's
+  // routing loads are not held up long behind it).
+  if constexpr (kShared) {
+    const int pa = split_at(Is, sw, nsw), pb = split_at(Is, sw + 1, nsw);
+    XFrag<kBF16> xb[CH];
+    frags_of<kBF16, CH>(xb_raw, xb);
+    for (int p = pa; p < pb; ++p) {
+      RowLoad<kBF16, CH> rg, ru;
+      issue_row<kBF16, CH>(a.sg_w + p * rowH16, nullptr, colH16, rg);
+      issue_row<kBF16, CH>(a.su_w + p * rowH16, nullptr, colH16, ru);
+      float v[2] = {dot_row<kBF16, CH>(rg, xb, colH16), dot_row<kBF16, CH>(ru, xb, colH16)};
+      const float sum = wave_multi_sum<2>(v);  // lanes 0-31: gate, 32-63: up
+      const float up = xor_partner<32>(sum);
+      if (lane == 0)
+        co_store<uint32_t>(a.hs + p, tag16(epoch_after(sum), f32_to_bf16(silu(round_bf16(sum)) * round_bf16(up))));
     }
   }
+  XFrag<ENC> xr[CHR];
+  frags_of<ENC, CHR>(xr_raw, xr);
+  UQM_FUSED_TRACE(4);
+  lds_barrier();  // routes ready
+  const int route_e = lane < k ? l_route[lane] : 0;
+  UQM_FUSED_TRACE(5);
+
+  // Phase B: routed gate+up row pairs q = slot * I + i, RBP pairs per batch.
+  const int nq = k * I;
+  const int qa = split_at(nq, sw, nsw), qb = split_at(nq, sw + 1, nsw);
+  RowLoad<ENC, CHR> rb[RBP][2];
+  // Always issues RBP pairs (pairs past n re-read pair n - 1, which is then
+  // still in flight, so the repeat costs no HBM traffic): a fixed count keeps
+  // the compiler's waits for each pair exact, so computing the pairs never
+  // waits for loads issued after them.
+  auto issue_b = [&](int q0, int n) {
+    int slot = q0 / I, i = q0 - slot * I;
+#pragma unroll
+    for (int t = 0; t < RBP; ++t) {
+      const int64_t e = lane_value(route_e, slot);
+      const int64_t grow = e * I + i;
+      const int64_t srow = e * spe + static_cast<int64_t>(i) * hpg;
+      issue_row<ENC, CHR>(a.eg + grow * rowHR, a.egs + srow, colHR, rb[t][0]);
+      issue_row<ENC, CHR>(a.eu + grow * rowHR, a.eus + srow, colHR, rb[t][1]);
+      if (t + 1 < n && ++i == I) {
+        i = 0;
+        ++slot;
+      }
+    }
+  };
+  // Every issued pair is reduced (only the stores depend on n): a load whose
+  // value were used under a branch could be sunk into it by the compiler,
+  // behind loads issued later.
+  auto compute_b = [&](int q0, int n) {
+    float v[VB];
+#pragma unroll
+    for (int t = 0; t < RBP; ++t) {
+      v[2 * t] = dot_row<ENC, CHR>(rb[t][0], xr, colHR);
+      v[2 * t + 1] = dot_row<ENC, CHR>(rb[t][1], xr, colHR);
+    }
+#pragma unroll
+    for (int t = 2 * RBP; t < VB; ++t) v[t] = 0.f;
+    const float sum = wave_multi_sum<VB>(v);  // value lane >> (6 - log2 VB): gate t, up t, ...
+    const float up = xor_partner<64 / VB>(sum);
+    constexpr int kL = log2_of<VB>();
+    const int idx = lane >> (6 - kL);
+    const int t = idx >> 1;
+    if ((lane & ((64 >> kL) - 1)) == 0 && (idx & 1) == 0 && t < n)
+      co_store<uint32_t>(a.hr + q0 + t, tag16(epoch_after(sum), f32_to_bf16(silu(round_bf16(sum)) * round_bf16(up))));
+  };
+
+  // Phase C: output rows o in [oa, ob): the shared down row (CISX chunks per
+  // lane) and the k routed down rows flattened into k * CR chunk jobs, job
+  // lane + 64 t of this lane.
+  const int oa = split_at(H, sw, nsw), ob = split_at(H, sw + 1, nsw);
+  Cols<kBF16, CISX> colIS;
+  make_cols<kBF16, CISX>(kShared ? Is / 8 : 0, 1, colIS);
+  const int njw = uniform((jobs + 63) >> 6);  // job rounds of this wave (<= NJ)
+  // Job lane + 64 t: (index clamped to 0 past the end, slot, chunk). The slot
+  // comes from a float reciprocal: exact here (jobs < 2^13, and the quotient
+  // is never within 1/(2 CR) of an integer boundary).
+  const float rcp_cr = 1.0f / static_cast<float>(CR);
+  struct Job {
+    int jj, s, c;
+    bool ok;
+  };
+  auto job = [&](int t) {
+    Job r;
+    const int j = lane + 64 * t;
+    r.ok = j < jobs;
+    r.jj = r.ok ? j : 0;
+    r.s = static_cast<int>((static_cast<float>(r.jj) + 0.5f) * rcp_cr);
+    r.c = r.jj - r.s * CR;
+    return r;
+  };
+  RowLoad<kBF16, CISX> rs;
+  uint4 rw[NJ];
+  float rsc[NJ];
+  auto issue_cs = [&](int o, const Cols<kBF16, CISX>& cis) {
+    if constexpr (kShared) issue_row<kBF16, CISX>(a.sd_w + static_cast<int64_t>(o) * rowIS, nullptr, cis, rs);
+  };
+  auto issue_cr = [&](int o) {
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) {
+      if (t < njw) {
+        const Job jt = job(t);
+        const int64_t e = l_route[jt.s];
+        rw[t] = ld_stream(a.ed + (e * H + o) * rowIR + static_cast<uint32_t>(jt.c * 16));
+        if constexpr (ER::kScaled)
+          rsc[t] = ld_stream(a.eds + e * spd + static_cast<int64_t>(o) * ipg +
+                             static_cast<uint32_t>((jt.c * ER::kElems) / group));
+      }
+    }
+  };
+
+  int q0 = qa;
+  for (; qb - q0 > RBP; q0 += RBP) {
+    issue_b(q0, RBP);
+    compute_b(q0, RBP);
+  }
+  // Issued unconditionally (a wave without pairs or rows re-reads a valid
+  // one) so that the waits stay exact, as above.
+  const int n = qb - q0;
+  issue_b(n > 0 ? q0 : nq - 1, n > 0 ? n : 1);
+  issue_cs(oa < ob ? oa : H - 1, colIS);
+  compute_b(q0, n);
+  UQM_FUSED_TRACE(6);
+  issue_cr(oa < ob ? oa : H - 1);
+  UQM_FUSED_TRACE(10);
+
+  // Stage every SiLU product into LDS: this wave's share of the 64-bit tag
+  // pairs, reloaded until all carry this launch's epoch. The first load waits
+  // behind the phase-C rows already in flight, by when the products are
+  // normally all published.
+  {
+    const uint32_t epoch = next_epoch(last_epoch);
+    const int n2 = (Is + k * I) / 2;
+    uint32_t* lh32 = reinterpret_cast<uint32_t*>(lhs);
+    const uint64_t* hs64 = reinterpret_cast<const uint64_t*>(a.hs);
+    const uint64_t* hr64 = reinterpret_cast<const uint64_t*>(a.hr);
+    const int is2 = Is / 2;
+    for (int r0 = wave * 64; r0 < n2; r0 += SL * kWaves * 64) {
+      const int base = r0 + lane;
+      uint64_t v[SL];
+      for (uint32_t spins = 0;; ++spins) {
+        // All SL loads are issued before any is checked (lanes past the end
+        // re-read the last pair and are not checked).
+#pragma unroll
+        for (int t = 0; t < SL; ++t) {
+          const int j = min(base + t * kWaves * 64, n2 - 1);
+          v[t] = co_load(j < is2 ? hs64 + j : hr64 + (j - is2));
+        }
+        bool ok = true;
+#pragma unroll
+        for (int t = 0; t < SL; ++t) {
+          const bool tagged = static_cast<uint32_t>(v[t] >> 48) == epoch &&
+                              (static_cast<uint32_t>(v[t]) >> 16) == epoch;
+          ok &= tagged | (base + t * kWaves * 64 >= n2);
+        }
+        if (__all(ok)) break;
+        if (spins > kSpinLimit) {
+          if (lane == 0) atomicOr(error, 1u);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+#pragma unroll
+      for (int t = 0; t < SL; ++t) {
+        const int j = base + t * kWaves * 64;
+        if (j < n2) lh32[j] = (static_cast<uint32_t>(v[t]) & 0xFFFFu) | (static_cast<uint32_t>(v[t] >> 32) << 16);
+      }
+    }
+  }
+  UQM_FUSED_TRACE(7);
+  lds_barrier();  // SiLU products staged
+  build_fragments();
+  lds_barrier();  // routed fragments built
+  UQM_FUSED_TRACE(8);
+
+  float sg = 0.f;
+  if constexpr (kShared) sg = *l_sg;
+  // out[o] = bf16(sum over lanes of (sg * shared partial + routed partial)).
+  auto compute_c = [&](int o, bool store, const Cols<kBF16, CISX>& cis) {
+    float acc = 0.f;
+    if constexpr (kShared) {
+      XFrag<kBF16> fs[CISX];
+      frags_from<kBF16, CISX>(lhs, cis, fs);
+      acc = sg * dot_row<kBF16, CISX>(rs, fs, cis);
+    }
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) {
+      if (t < njw) {
+        const Job jt = job(t);
+        XFrag<ENC> f;
+#pragma unroll
+        for (int q = 0; q < ER::kXWords / 4; ++q) {
+          const uint4 u = *reinterpret_cast<const uint4*>(lfr + jt.jj * ER::kXWords + 4 * q);
+          f.w[4 * q] = u.x;
+          f.w[4 * q + 1] = u.y;
+          f.w[4 * q + 2] = u.z;
+          f.w[4 * q + 3] = u.w;
+        }
+        f.off = loff[jt.jj];
+        const float w = jt.ok ? l_w[jt.s] : 0.f;
+        const float d = dot_chunk<ENC>(rw[t], f);
+        acc = fmaf(d, ER::kScaled ? rsc[t] * w : w, acc);
+      }
+    }
+    const float y = wave_sum(acc);
+    if (lane == 0 && store) a.out[o] = f32_to_bf16(y);
+  };
+  compute_c(oa < ob ? oa : H - 1, oa < ob, colIS);  // unconditional, as compute_b
+  for (int o = oa + 1; o < ob; ++o) {  // more rows than streaming waves (small grids only)
+    Cols<kBF16, CISX> cis;
+    make_cols<kBF16, CISX>(kShared ? Is / 8 : 0, 1, cis, opaque_lane());
+    issue_cs(o, cis);
+    issue_cr(o);
+    compute_c(o, true, cis);
+  }
+  UQM_FUSED_TRACE(9);
 }
 
 namespace {
 
 int cpl(int64_t chunks) { return static_cast<int>((chunks + 63) / 64); }
 
-size_t lds_bytes(const FusedArgs& a, int kmax) {
-  const size_t routed = kRoutedLdsHeader + static_cast<size_t>(kmax) * a.I * 2;
-  const size_t shared = ((2 * static_cast<size_t>(a.Is) + 15) & ~static_cast<size_t>(15)) + 16;
-  return routed > shared ? routed : shared;
-}
 
 template <int ENC, int CH, int CHR, int CIR, int CIS, int KMAX>
-hipError_t launch_cfg(const FusedArgs& args, int routed_blocks, hipStream_t stream) {
+hipError_t launch_cfg(const FusedArgs& args, hipStream_t stream) {
   auto kern = moe_decode_fused_kernel<ENC, CH, CHR, CIR, CIS, KMAX>;
-  const size_t lds = lds_bytes(args, KMAX);
+  const size_t lds = fused_lds_bytes<ENC>(args.I, args.Is, args.k);
   if (lds > 64 * 1024) return hipErrorInvalidValue;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -564,48 +773,42 @@ hipError_t launch_cfg(const FusedArgs& args, int routed_blocks, hipStream_t stre
   int per_cu = 0, cus = 0;
   if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, lds)) != hipSuccess) return e;
   if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-  if (per_cu < 1 || cus < 2) return hipErrorInvalidConfiguration;
-  FusedArgs a = args;
-  const int blocks = cus;  // one workgroup per CU, all resident
-  a.routed_blocks = CIS > 0 ? (routed_blocks > 0 && routed_blocks < blocks ? routed_blocks : blocks / 2) : blocks;
-  hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), lds, stream, a);
+  if (per_cu < 1 || cus < 1 || cus > kMaxFusedBlocks) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(kern, dim3(cus), dim3(kThreads), lds, stream, args);  // one workgroup per CU, all resident
   return hipGetLastError();
 }
 
 }  // namespace
 
-int fused_config_id(int enc, int64_t H, int64_t I, int64_t Is, int64_t k) {
+int fused_config_id(int enc, int64_t H, int64_t I, int64_t Is, int64_t k, int64_t E) {
   // Per-lane chunk loops are masked, so an instantiation serves every shape
   // whose chunk counts per lane do not exceed its template arguments.
   const int el = enc == kQ4 ? 32 : enc == kQ8 ? 16 : 8;
   const int ch = cpl(H / 8), chr = cpl(H / el), cir = cpl(I / el), cis = Is > 0 ? cpl(Is / 8) : 0;
-  if (k < 1 || k > 8 || ch > 4 || cis > 11) return -1;
-  if (kRoutedLdsHeader + (k <= 4 ? 4 : 8) * I * 2 > 64 * 1024 || Is * 2 + 32 > 64 * 1024) return -1;
+  if (k < 1 || k > 8 || k > E || E < 1 || E + 1 > 320 || ch > 4 || cis > 11) return -1;
+  // Instantiations whose rows all fit in registers (others run the
+  // multi-kernel path): Q4 with a shared expert and k <= 4 or without one and
+  // k <= 8; Q8 and BF16 without a shared expert and k <= 4.
+  if (enc == kQ4 ? (Is > 0 && k > 4) : (Is > 0 || k > 4)) return -1;
+  if (H % 8 != 0 || I % 8 != 0 || Is % 8 != 0) return -1;
+  const size_t lds = enc == kQ4 ? fused_lds_bytes<kQ4>(I, Is, k)
+                                 : enc == kQ8 ? fused_lds_bytes<kQ8>(I, Is, k) : fused_lds_bytes<kBF16>(I, Is, k);
+  if (lds > 64 * 1024) return -1;
   if (enc == kQ4 && chr <= 1 && cir <= 1) return 0;
   if (enc == kQ8 && chr <= 2 && cir <= 2) return 1;
   if (enc == kBF16 && chr <= 4 && cir <= 3) return 2;
   return -1;
 }
 
-hipError_t launch_moe_decode_fused(int enc, const FusedArgs& a, int routed_blocks, hipStream_t stream) {
-  if (fused_config_id(enc, a.H, a.I, a.Is, a.k) < 0) return hipErrorInvalidValue;
-  const bool shared = a.Is > 0;
+hipError_t launch_moe_decode_fused(int enc, const FusedArgs& a, hipStream_t stream) {
+  if (fused_config_id(enc, a.H, a.I, a.Is, a.k, a.E) < 0) return hipErrorInvalidValue;
   const bool k4 = a.k <= 4;
-#define UQM_FUSED(ENCV, CHR, CIR)                                                                 \
-  if (shared) {                                                                                    \
-    return k4 ? launch_cfg<ENCV, 4, CHR, CIR, 11, 4>(a, routed_blocks, stream)                     \
-              : launch_cfg<ENCV, 4, CHR, CIR, 11, 8>(a, routed_blocks, stream);                    \
-  }                                                                                                \
-  return k4 ? launch_cfg<ENCV, 4, CHR, CIR, 0, 4>(a, routed_blocks, stream)                        \
-            : launch_cfg<ENCV, 4, CHR, CIR, 0, 8>(a, routed_blocks, stream);
   if (enc == kQ4) {
-    UQM_FUSED(kQ4, 1, 1)
+    if (a.Is > 0) return launch_cfg<kQ4, 4, 1, 1, 11, 4>(a, stream);
+    return k4 ? launch_cfg<kQ4, 4, 1, 1, 0, 4>(a, stream) : launch_cfg<kQ4, 4, 1, 1, 0, 8>(a, stream);
   }
-  if (enc == kQ8) {
-    UQM_FUSED(kQ8, 2, 2)
-  }
-  UQM_FUSED(kBF16, 4, 3)
-#undef UQM_FUSED
+  if (enc == kQ8) return launch_cfg<kQ8, 4, 2, 2, 0, 4>(a, stream);
+  return launch_cfg<kBF16, 4, 4, 3, 0, 4>(a, stream);
 }
 
 }  // namespace uqm

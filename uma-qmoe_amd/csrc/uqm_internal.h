@@ -122,11 +122,12 @@ hipError_t launch_combine(const float* y, int y_parts, int64_t y_stride, const u
                           const int64_t* indices, int64_t T, int64_t k, int64_t E, int64_t H, const float* ys,
                           int ys_parts, int64_t ys_stride, const float* sg, uint16_t* out, hipStream_t stream);
 // Single-token fused MoE block (uqm_fused.hip). Sync words live in `sync`
-// (zero before the first launch): an epoch that the kernel advances on every
-// launch, a finished-workgroup counter it returns to zero, and a sticky error
-// word it raises when one of its bounded waits expires.
-enum : int { kSyncEpoch = 0, kSyncBlocksDone = 1, kSyncError = 4 };
-constexpr int kSyncWords = 64;
+// (zero before the first launch): a sticky error word the kernel raises when
+// one of its bounded waits expires, and one launch epoch per workgroup that
+// the workgroup advances on every launch.
+enum : int { kSyncError = 4, kSyncEpochBase = 64 };
+constexpr int kMaxFusedBlocks = 1024;  // workgroups (one per CU)
+constexpr int kSyncWords = kSyncEpochBase + kMaxFusedBlocks;
 
 struct FusedArgs {
   const uint16_t* x;                   // [H] bf16, 16-byte aligned
@@ -143,22 +144,20 @@ struct FusedArgs {
   const float* eds;
   int64_t H, I, Is;
   int E, k, group, norm;
-  int routed_blocks;                   // set by the launcher
   uint32_t* sync;                      // kSyncWords words
-  uint32_t* hs;                        // [Is] epoch-tagged shared SiLU products
-  uint32_t* hr;                        // [k, I] epoch-tagged routed SiLU products
-  uint64_t* yr;                        // [H] epoch-tagged routed outputs (fp32)
+  uint32_t* hs;                        // [Is] epoch-tagged shared SiLU products (8-byte aligned)
+  uint32_t* hr;                        // [k, I] epoch-tagged routed SiLU products (8-byte aligned)
+  uint64_t* lgt;                       // [E + 1] epoch-tagged router logits (fp32), shared gate last
   uint16_t* out;                       // [H]
   uint16_t* logits_out;                // optional [E]
   uint16_t* weights_out;               // optional [k]
   int64_t* indices_out;                // optional [k]
 };
 
-// Returns >= 0 when a compiled instantiation covers (encoding, H, I, Is, k).
-int fused_config_id(int enc, int64_t H, int64_t I, int64_t Is, int64_t k);
-// routed_blocks: CUs given to the routed experts when a shared expert is
-// present (0 = half of the CUs).
-hipError_t launch_moe_decode_fused(int enc, const FusedArgs& a, int routed_blocks, hipStream_t stream);
+// Returns >= 0 when a compiled instantiation covers (encoding, H, I, Is, k, E).
+int fused_config_id(int enc, int64_t H, int64_t I, int64_t Is, int64_t k, int64_t E);
+// One workgroup per CU; needs every workgroup resident at once.
+hipError_t launch_moe_decode_fused(int enc, const FusedArgs& a, hipStream_t stream);
 
 hipError_t launch_rmsnorm(const uint16_t* x, int64_t rows, int64_t H, const uint16_t* weight, float eps,
                           uint16_t* out, hipStream_t stream);
