@@ -140,26 +140,34 @@ __device__ __forceinline__ void make_frag(const uint32_t* raw, XFrag<ENC>& f) {
 template <int ENC>
 __device__ __forceinline__ float dot_chunk(const uint4 wv, const XFrag<ENC>& f) {
   const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
+  // ((w >> s) & 0x000F000F) ^ K puts two fields into the low bits of two bf16
+  // halves whose high bits read 0x43 (128.0), flipping field bit 3 where K
+  // has 0x8: one shift and one v_bitop3 per bf16 pair.
+  constexpr uint32_t kM = 0x000F000Fu;
   if constexpr (ENC == kQ4) {
+    constexpr uint32_t kK = 0x43084308u;  // field u = nibble ^ 8
     float acc = f.off;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      const uint32_t u = w4[d] ^ 0x88888888u;
-      acc = dot2((u & 0x000F000Fu) | 0x43004300u, f.w[4 * d + 0], acc);
-      acc = dot2(((u >> 4) & 0x000F000Fu) | 0x43004300u, f.w[4 * d + 1], acc);
-      acc = dot2(((u >> 8) & 0x000F000Fu) | 0x43004300u, f.w[4 * d + 2], acc);
-      acc = dot2(((u >> 12) & 0x000F000Fu) | 0x43004300u, f.w[4 * d + 3], acc);
+      const uint32_t w = w4[d];
+      acc = dot2((w & kM) ^ kK, f.w[4 * d + 0], acc);
+      acc = dot2(((w >> 4) & kM) ^ kK, f.w[4 * d + 1], acc);
+      acc = dot2(((w >> 8) & kM) ^ kK, f.w[4 * d + 2], acc);
+      acc = dot2(((w >> 12) & kM) ^ kK, f.w[4 * d + 3], acc);
     }
     return acc;
   } else if constexpr (ENC == kQ8) {
+    // byte ^ 0x80 = 16 * hi + lo: the low nibble is unchanged, bit 3 of the
+    // high nibble flips.
+    constexpr uint32_t kLo = 0x43004300u, kHi = 0x43084308u;
     float lo = 0.f, hi = 0.f;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      const uint32_t u = w4[d] ^ 0x80808080u;
-      lo = dot2((u & 0x000F000Fu) | 0x43004300u, f.w[2 * d + 0], lo);
-      lo = dot2(((u >> 8) & 0x000F000Fu) | 0x43004300u, f.w[2 * d + 1], lo);
-      hi = dot2(((u >> 4) & 0x000F000Fu) | 0x43004300u, f.w[2 * d + 0], hi);
-      hi = dot2(((u >> 12) & 0x000F000Fu) | 0x43004300u, f.w[2 * d + 1], hi);
+      const uint32_t w = w4[d];
+      lo = dot2((w & kM) ^ kLo, f.w[2 * d + 0], lo);
+      lo = dot2(((w >> 8) & kM) ^ kLo, f.w[2 * d + 1], lo);
+      hi = dot2(((w >> 4) & kM) ^ kHi, f.w[2 * d + 0], hi);
+      hi = dot2(((w >> 12) & kM) ^ kHi, f.w[2 * d + 1], hi);
     }
     return lo + 16.0f * hi + f.off;
   } else {

@@ -63,7 +63,9 @@ constexpr int kWaves = 8;                  // streaming waves per workgroup
 constexpr int kThreads = (kWaves + 1) * 64;  // + the control wave
 constexpr int kLdsHeader = 256;            // flags, routes, weights, shared gate (16-byte aligned)
 constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a wait gives up (well over 0.1 s)
-constexpr int kPollSleep = 8;              // s_sleep units (64 clocks) between router logit polls
+constexpr int kPollSleep = 40;             // s_sleep units (64 clocks) between router logit polls
+constexpr int kPollDelay = 64;             // s_sleep units before the first poll (the logits cannot be
+                                           // in sooner; fewer polls leave more bandwidth to phase A)
 constexpr int kRouterHeadStart = 12;       // s_sleep units the streaming waves of router workgroups yield
 #ifndef UQM_FUSED_CTRL_PRIO
 #define UQM_FUSED_CTRL_PRIO 3
@@ -115,12 +117,13 @@ __device__ __forceinline__ uint64_t tag32(uint32_t epoch, float v) {
 template <int ENC, int CPL>
 struct Cols {
   int C, ln;
+  bool full;  // C == 64 * CPL (wave-uniform): no chunk is clamped or masked
   int sc[Enc<ENC>::kScaled ? CPL : 1];
   __device__ __forceinline__ int c(int j) const {
     const int v = ln + 64 * j;
-    return v < C ? v : 0;
+    return full || v < C ? v : 0;
   }
-  __device__ __forceinline__ float m(int j) const { return ln + 64 * j < C ? 1.f : 0.f; }
+  __device__ __forceinline__ float m(int j) const { return full || ln + 64 * j < C ? 1.f : 0.f; }
   __device__ __forceinline__ int s(int j) const {
     if constexpr (Enc<ENC>::kScaled) return sc[j];
     return 0;
@@ -155,6 +158,7 @@ __device__ __forceinline__ uint32_t pinned_after(uint32_t v, float dep) {
 template <int ENC, int CPL>
 __device__ __forceinline__ void make_cols(int C, int group, Cols<ENC, CPL>& cl, int ln = -1) {
   cl.C = C;
+  cl.full = C == 64 * CPL;
   cl.ln = ln >= 0 ? ln : static_cast<int>(threadIdx.x & 63);
   if constexpr (Enc<ENC>::kScaled) {
 #pragma unroll
@@ -223,6 +227,11 @@ template <int ENC, int CPL>
 __device__ __forceinline__ float dot_row(const RowLoad<ENC, CPL>& r, const XFrag<ENC> (&f)[CPL],
                                          const Cols<ENC, CPL>& cl) {
   float acc = 0.f;
+  if (cl.full && !Enc<ENC>::kScaled) {  // unscaled rows filling every lane: plain sum
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) acc += dot_chunk<ENC>(r.w[j], f[j]);
+    return acc;
+  }
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const float d = dot_chunk<ENC>(r.w[j], f[j]);
@@ -304,9 +313,10 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   // Routed down chunks per lane: the k rows of an output row are flattened
   // over the wave's lanes (k * CR chunks).
   constexpr int NJ = KMAX * CIR;
-  // 64-bit tag loads per lane per staging round (fewer when many routed down
-  // chunks are held in registers)
-  constexpr int SL = NJ > 4 ? 4 : 12;
+  // 64-bit tag loads per lane per staging round: one round covers 3072 pairs
+  // (6144 products: the shared or the routed products of c2) with a shared
+  // expert, 4096 pairs without (the routed products of c1).
+  constexpr int SL = kShared ? 6 : 8;
   constexpr int LPL = 5;  // router logits per lane: E + 1 <= 320
   extern __shared__ __align__(16) unsigned char lds[];
   const int H = static_cast<int>(a.H), I = static_cast<int>(a.I), Is = kShared ? static_cast<int>(a.Is) : 0;
@@ -396,10 +406,11 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     const uint32_t epoch = next_epoch(last_epoch);
     UQM_FUSED_TRACE(1);
     // Every logit, once all its producers have published it. Three polls are
-    // kept in flight, a short sleep apart, so a late producer is seen one
-    // spacing (not one round trip) after it publishes; every poll issues the
-    // same loads (lanes past the end re-read the last word), which keeps the
-    // compiler's waits for the oldest poll exact.
+    // kept in flight, ~1 us apart, so a late producer is seen one spacing (not
+    // one round trip) after it publishes; every poll issues the same loads
+    // (lanes past the end re-read the last word), which keeps the compiler's
+    // waits for the oldest poll exact. (All 256 control waves poll the same
+    // few lines: polling more often measurably slows the streaming phases.)
     uint64_t pa[LPL], pb[LPL], pc[LPL];
     auto poll = [&](uint64_t (&t)[LPL]) {
 #pragma unroll
@@ -416,6 +427,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
 #pragma unroll
       for (int j = 0; j < LPL; ++j) lv[j] = __uint_as_float(static_cast<uint32_t>(t[j]));
     };
+    __builtin_amdgcn_s_sleep(kPollDelay);
     poll(pa);
     __builtin_amdgcn_s_sleep(kPollSleep);
     poll(pb);
@@ -509,7 +521,9 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     }
     UQM_FUSED_TRACE(3);
     lds_barrier();  // routes ready
-    lds_barrier();  // SiLU products staged
+    lds_barrier();  // routed gate/up rows issued
+    lds_barrier();  // shared products staged
+    lds_barrier();  // routed products staged
     build_fragments();
     lds_barrier();  // routed fragments built
     if (lane == 0) co_store<uint32_t>(my_epoch, epoch);
@@ -558,6 +572,8 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   XFrag<ENC> xr[CHR];
   frags_of<ENC, CHR>(xr_raw, xr);
   UQM_FUSED_TRACE(4);
+  // All waves move to phase B together (one workgroup barrier; letting each
+  // wave start phase B on its own, through an LDS flag, measured slower).
   lds_barrier();  // routes ready
   const int route_e = lane < k ? l_route[lane] : 0;
   UQM_FUSED_TRACE(5);
@@ -621,12 +637,18 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     int jj, s, c;
     bool ok;
   };
+  int jjs_[NJ], js_[NJ];  // job index (0 past the end) and slot; -1 slot past the end
+#pragma unroll
+  for (int t = 0; t < NJ; ++t) {
+    const int j = lane + 64 * t;
+    jjs_[t] = j < jobs ? j : 0;
+    js_[t] = j < jobs ? static_cast<int>((static_cast<float>(jjs_[t]) + 0.5f) * rcp_cr) : -1;
+  }
   auto job = [&](int t) {
     Job r;
-    const int j = lane + 64 * t;
-    r.ok = j < jobs;
-    r.jj = r.ok ? j : 0;
-    r.s = static_cast<int>((static_cast<float>(r.jj) + 0.5f) * rcp_cr);
+    r.ok = js_[t] >= 0;
+    r.jj = jjs_[t];
+    r.s = r.ok ? js_[t] : 0;
     r.c = r.jj - r.s * CR;
     return r;
   };
@@ -657,73 +679,95 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   }
   // Issued unconditionally (a wave without pairs or rows re-reads a valid
   // one) so that the waits stay exact, as above.
+  // The routed products are what every CU waits for, and scattered 1 KB rows
+  // lose out at the memory controllers to long sequential streams. So every
+  // wave issues its routed gate/up rows, and computes and publishes its routed
+  // products, before it issues its routed down rows and its 11 KB shared down
+  // row (measured: issuing the shared down row with the routed rows, or at
+  // kernel start, is 2-4 us slower per call).
   const int n = qb - q0;
   issue_b(n > 0 ? q0 : nq - 1, n > 0 ? n : 1);
-  issue_cs(oa < ob ? oa : H - 1, colIS);
+  lds_barrier();  // routed gate/up rows issued
   compute_b(q0, n);
   UQM_FUSED_TRACE(6);
-  issue_cr(oa < ob ? oa : H - 1);
-  UQM_FUSED_TRACE(10);
 
-  // Stage every SiLU product into LDS: this wave's share of the 64-bit tag
-  // pairs, reloaded until all carry this launch's epoch. The first load waits
-  // behind the phase-C rows already in flight, by when the products are
-  // normally all published.
-  {
-    const uint32_t epoch = next_epoch(last_epoch);
-    const int n2 = (Is + k * I) / 2;
-    uint32_t* lh32 = reinterpret_cast<uint32_t*>(lhs);
-    const uint64_t* hs64 = reinterpret_cast<const uint64_t*>(a.hs);
-    const uint64_t* hr64 = reinterpret_cast<const uint64_t*>(a.hr);
-    const int is2 = Is / 2;
-    for (int r0 = wave * 64; r0 < n2; r0 += SL * kWaves * 64) {
-      const int base = r0 + lane;
-      uint64_t v[SL];
+  // Staging of SiLU products into LDS: each wave takes 64-bit tag pairs
+  // r0 + lane + 512 t (t < SL) of a round, reloads until all carry this
+  // launch's epoch, and stores the bf16 pairs. The shared products (published
+  // since phase A) are loaded before the phase-C rows, so they are in LDS by
+  // the time the shared down row arrives; the routed products are loaded
+  // after them and are the last thing the wave waits for.
+  const uint32_t epoch = next_epoch(last_epoch);
+  constexpr int kRound = SL * kWaves * 64;
+  auto load_round = [&](const uint64_t* src, int n2, int base, uint64_t (&v)[SL]) {
+#pragma unroll
+    for (int t = 0; t < SL; ++t) v[t] = co_load(src + min(base + t * kWaves * 64, n2 - 1));
+  };
+  auto round_ok = [&](int n2, int base, const uint64_t (&v)[SL]) {
+    bool ok = true;
+#pragma unroll
+    for (int t = 0; t < SL; ++t) {
+      const bool tagged = static_cast<uint32_t>(v[t] >> 48) == epoch && (static_cast<uint32_t>(v[t]) >> 16) == epoch;
+      ok &= tagged | (base + t * kWaves * 64 >= n2);
+    }
+    return __all(ok) != 0;
+  };
+  auto finish_round = [&](const uint64_t* src, int n2, int base, uint32_t* dst, uint64_t (&v)[SL]) {
+    // The first check is outside the retry loop, so the compiler waits for
+    // exactly these loads (not for the rows issued after them).
+    if (!round_ok(n2, base, v)) {
       for (uint32_t spins = 0;; ++spins) {
-        // All SL loads are issued before any is checked (lanes past the end
-        // re-read the last pair and are not checked).
-#pragma unroll
-        for (int t = 0; t < SL; ++t) {
-          const int j = min(base + t * kWaves * 64, n2 - 1);
-          v[t] = co_load(j < is2 ? hs64 + j : hr64 + (j - is2));
-        }
-        bool ok = true;
-#pragma unroll
-        for (int t = 0; t < SL; ++t) {
-          const bool tagged = static_cast<uint32_t>(v[t] >> 48) == epoch &&
-                              (static_cast<uint32_t>(v[t]) >> 16) == epoch;
-          ok &= tagged | (base + t * kWaves * 64 >= n2);
-        }
-        if (__all(ok)) break;
         if (spins > kSpinLimit) {
           if (lane == 0) atomicOr(error, 1u);
           break;
         }
         __builtin_amdgcn_s_sleep(2);
-      }
-#pragma unroll
-      for (int t = 0; t < SL; ++t) {
-        const int j = base + t * kWaves * 64;
-        if (j < n2) lh32[j] = (static_cast<uint32_t>(v[t]) & 0xFFFFu) | (static_cast<uint32_t>(v[t] >> 32) << 16);
+        load_round(src, n2, base, v);
+        if (round_ok(n2, base, v)) break;
       }
     }
+#pragma unroll
+    for (int t = 0; t < SL; ++t) {
+      const int j = base + t * kWaves * 64;
+      if (j < n2) dst[j] = (static_cast<uint32_t>(v[t]) & 0xFFFFu) | (static_cast<uint32_t>(v[t] >> 32) << 16);
+    }
+  };
+  const uint64_t* hs64 = reinterpret_cast<const uint64_t*>(a.hs);
+  const uint64_t* hr64 = reinterpret_cast<const uint64_t*>(a.hr);
+  const int n2s = Is / 2, n2r = k * I / 2;
+  const int base0 = wave * 64 + lane;
+  uint64_t vs[SL];
+  if constexpr (kShared) load_round(hs64, n2s, base0, vs);
+  issue_cr(oa < ob ? oa : H - 1);
+  issue_cs(oa < ob ? oa : H - 1, colIS);
+  if constexpr (kShared) {
+    finish_round(hs64, n2s, base0, reinterpret_cast<uint32_t*>(lhs), vs);
+    for (int b2 = base0 + kRound; b2 - lane < n2s; b2 += kRound) {
+      load_round(hs64, n2s, b2, vs);
+      finish_round(hs64, n2s, b2, reinterpret_cast<uint32_t*>(lhs), vs);
+    }
   }
+  uint64_t vr[SL];
+  load_round(hr64, n2r, base0, vr);
   UQM_FUSED_TRACE(7);
-  lds_barrier();  // SiLU products staged
-  build_fragments();
-  lds_barrier();  // routed fragments built
-  UQM_FUSED_TRACE(8);
+  lds_barrier();  // shared products staged
 
   float sg = 0.f;
   if constexpr (kShared) sg = *l_sg;
-  // out[o] = bf16(sum over lanes of (sg * shared partial + routed partial)).
-  auto compute_c = [&](int o, bool store, const Cols<kBF16, CISX>& cis) {
+  // Shared part of out[o] (per lane): sg * (shared down row o . h_s).
+  auto shared_part = [&](const Cols<kBF16, CISX>& cis) {
     float acc = 0.f;
     if constexpr (kShared) {
       XFrag<kBF16> fs[CISX];
       frags_from<kBF16, CISX>(lhs, cis, fs);
       acc = sg * dot_row<kBF16, CISX>(rs, fs, cis);
     }
+    return acc;
+  };
+  // Routed part of out[o] (per lane): sum over this lane's jobs of
+  // w_slot * scale * (down chunk . h_slot chunk).
+  auto routed_part = [&]() {
+    float acc = 0.f;
 #pragma unroll
     for (int t = 0; t < NJ; ++t) {
       if (t < njw) {
@@ -743,16 +787,30 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
         acc = fmaf(d, ER::kScaled ? rsc[t] * w : w, acc);
       }
     }
-    const float y = wave_sum(acc);
-    if (lane == 0 && store) a.out[o] = f32_to_bf16(y);
+    return acc;
   };
-  compute_c(oa < ob ? oa : H - 1, oa < ob, colIS);  // unconditional, as compute_b
+  const float acc_s = shared_part(colIS);
+  finish_round(hr64, n2r, base0, reinterpret_cast<uint32_t*>(lhr), vr);
+  for (int b2 = base0 + kRound; b2 - lane < n2r; b2 += kRound) {
+    load_round(hr64, n2r, b2, vr);
+    finish_round(hr64, n2r, b2, reinterpret_cast<uint32_t*>(lhr), vr);
+  }
+  lds_barrier();  // routed products staged
+  build_fragments();
+  lds_barrier();  // routed fragments built
+  UQM_FUSED_TRACE(8);
+  // out[o] = bf16(sum over lanes of (shared part + routed part)).
+  {
+    const float y = wave_sum(acc_s + routed_part());
+    if (lane == 0 && oa < ob) a.out[oa] = f32_to_bf16(y);
+  }
   for (int o = oa + 1; o < ob; ++o) {  // more rows than streaming waves (small grids only)
     Cols<kBF16, CISX> cis;
     make_cols<kBF16, CISX>(kShared ? Is / 8 : 0, 1, cis, opaque_lane());
     issue_cs(o, cis);
     issue_cr(o);
-    compute_c(o, true, cis);
+    const float y = wave_sum(shared_part(cis) + routed_part());
+    if (lane == 0) a.out[o] = f32_to_bf16(y);
   }
   UQM_FUSED_TRACE(9);
 }
