@@ -94,13 +94,28 @@ def cpu_baseline(shape, seconds: float):
 BASELINE_METRIC = "MoE layer \u00b5s/token + achieved HBM GB/s (% peak), Qwen-MoE shape, batch 1 & 32"
 
 
+# Sources of the single-token fused kernel: a profile of it stays valid while
+# these hash to the digest recorded with the measurement.
+FUSED_KERNEL_SOURCES = ("uqm_fused.hip", "uqm_device.h", "uqm_internal.h")
+
+
+def fused_kernel_source_sha256() -> str:
+    """SHA-256 over FUSED_KERNEL_SOURCES (name, NUL, bytes, in that order)."""
+    import hashlib
+
+    digest = hashlib.sha256()
+    for name in FUSED_KERNEL_SOURCES:
+        digest.update(name.encode("utf-8"))
+        digest.update(b"\0")
+        digest.update((ROOT / "uma-qmoe_amd" / "csrc" / name).read_bytes())
+    return digest.hexdigest()
+
+
 def profiled_traffic(workload: str):
     """HBM bytes per launch of the fused kernel from the committed rocprofv3
-    summary (profiles/moe_decode_fused_c2.md), only while the kernel sources
+    summary (profiles/moe_decode_fused_c2.md), only while the kernel's sources
     still hash to the digest recorded with the measurement."""
     import re
-
-    from uma_qmoe_amd.native_backend import native_kernel_source_sha256
 
     path = ROOT / "profiles" / "moe_decode_fused_c2.md"
     if not path.is_file():
@@ -109,7 +124,7 @@ def profiled_traffic(workload: str):
     if m is None:
         return None
     data = json.loads(m.group(1))
-    if data.get("workload") != workload or data.get("source_sha256") != native_kernel_source_sha256():
+    if data.get("workload") != workload or data.get("source_sha256") != fused_kernel_source_sha256():
         return None
     return int(data["traffic_bytes_per_launch"])
 
