@@ -37,9 +37,10 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=24)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c4", "c5"],
-                    help="c2 (default): Qwen W4A16 decode; c1: OLMoE decode; c4: Qwen prefill, 512 tokens; "
-                         "c5: 128-expert top-8 layer, 256 tokens with Zipf-skewed routes (routed experts only)")
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+                    help="c2 (default): Qwen W4A16 decode; c1: OLMoE decode; c3: 24-layer Qwen stack (BF16/Q8 routed "
+                         "experts), decode; c4: Qwen prefill, 512 tokens; c5: 128-expert top-8 layer, 256 tokens "
+                         "with Zipf-skewed routes (routed experts only)")
     ap.add_argument("--tokens", type=int, default=0, help="tokens per call (0: the config's own)")
     ap.add_argument("--rotate-bytes", type=float, default=1.1e9)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -230,6 +231,156 @@ def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
             "distinct_experts": sum(distinct) / len(distinct)}
 
 
+def measure_stack(torch, syn, ext, steps_per_rep: int, reps: int):
+    """c3: the 24-layer Qwen stack, one token, ``steps_per_rep`` decode steps
+    of x <- MoE_l(RMSNorm(x)) for l = 0..23 (routed BF16 in layers 0-15, Q8 in
+    16-23, BF16 shared expert in every layer; RMSNorm eps 1e-6, weight ones).
+    One step (24 norms + 24 blocks) is captured in a HIP graph that reads and
+    writes the same token buffer, so replays chain the steps. The ~22.6 GB of
+    weights are read once per step (no MALL reuse). Returns the median over
+    ``reps`` of the per-step time, for the fused single-token kernel and for
+    the multi-kernel path."""
+    from uma_qmoe_amd import _native
+
+    dev = torch.device("cuda:0")
+    shapes = [syn.c3_layer_shape(l) for l in range(syn.C3_LAYERS)]
+    layers = [syn.build_experts(s, layer=l, device=dev) for l, s in enumerate(shapes)]
+    denses = [syn.build_dense(s, layer=l, device=dev) for l, s in enumerate(shapes)]
+    s0 = shapes[0]
+    ws = ext._workspace(dev, 1, s0.hidden, s0.intermediate, s0.shared_intermediate, s0.num_experts, s0.top_k)
+    x0 = syn.hidden_states(s0, 1, device=dev, tag="c3_x0")
+    xbuf = x0.clone()
+    # one token routes to top_k distinct experts in every layer
+    algo = sum(syn.algorithmic_bytes(layers[l], denses[l], s.top_k) for l, s in enumerate(shapes))
+
+    def step():
+        for l, s in enumerate(shapes):
+            normed = ext.rmsnorm(xbuf, 1e-6)
+            res = ext.moe_layer(layers[l], denses[l], normed, s.top_k, out=xbuf, workspace=ws)
+        return res
+
+    out = {}
+    for mode, fused in (("fused", 1), ("multi_kernel", 0)):
+        ext.set_option(_native.UQM_OPT_FUSED_DECODE, fused)
+        xbuf.copy_(x0)
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        for _ in range(2):
+            graph.replay()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        samples = []
+        for _ in range(reps):
+            start.record()
+            for _ in range(steps_per_rep):
+                graph.replay()
+            stop.record()
+            torch.cuda.synchronize()
+            samples.append(start.elapsed_time(stop) * 1000.0 / steps_per_rep)
+        ext.workspace_status(ws)
+        if not bool(torch.isfinite(xbuf.float()).all()):
+            raise RuntimeError(f"c3 stack ({mode}) produced non-finite values")
+        out[mode] = sorted(samples)[len(samples) // 2]
+        del graph
+    ext.set_option(_native.UQM_OPT_FUSED_DECODE, 1)
+    del layers, denses, ws
+    torch.cuda.empty_cache()
+    return {"us_per_token": out["fused"], "multi_kernel_us_per_token": out["multi_kernel"], "bytes": algo,
+            "steps": steps_per_rep * reps}
+
+
+def cpu_baseline_stack(seconds: float):
+    """The oracle on the host cores for c3, sampled: one BF16 layer (layer 0)
+    and one Q8 layer (layer 16) are timed (median of repeated single-token
+    block calls, ~``seconds`` in all) and the stack is 16 x the first + 8 x the
+    second (the RMSNorms are < 0.1% and not counted)."""
+    import torch
+
+    from oracle import moe as om
+    from uma_qmoe_amd import synthetic as syn
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    med = {}
+    for layer in (0, 16):
+        shape = syn.c3_layer_shape(layer)
+        experts = syn.build_experts(shape, layer=layer)
+        dense = syn.build_dense(shape, layer=layer)
+        reader = syn.DeviceLayerReader({layer: experts})
+        lay = {"router": dense.router, "top_k": shape.top_k, "num_experts": shape.num_experts,
+               "shared_gate": dense.shared_gate, "shared_up": dense.shared_up, "shared_down": dense.shared_down,
+               "shared_expert_gate": dense.shared_expert_gate}
+        x = syn.hidden_states(shape, 1, tag="c3_x0")
+        om.qwen_block(x, lay, reader, layer)
+        times = []
+        start = time.perf_counter()
+        while time.perf_counter() - start < seconds / 2 or len(times) < 3:
+            t0 = time.perf_counter_ns()
+            om.qwen_block(x, lay, reader, layer)
+            times.append((time.perf_counter_ns() - t0) / 1e3)
+            if len(times) >= 100:
+                break
+        times.sort()
+        med[layer] = (times[len(times) // 2], len(times))
+        del experts, dense, reader
+    value = 16 * med[0][0] + 8 * med[16][0]
+    return {
+        "value": round(value, 1),
+        "unit": "us/token",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"16 x median of {med[0][1]} BF16 layer-0 block calls + 8 x median of {med[16][1]} Q8 layer-16 "
+                   "block calls (oracle, dequantize per call), single token"),
+    }
+
+
+def main_stack(args, torch, syn, ext) -> int:
+    # the default --steps (240) keeps c3's own 32 steps per timing; a smaller
+    # --steps is split over the 5 timings
+    reps = 5
+    steps_per_rep = syn.C3_STEPS if args.steps >= 240 else max(1, args.steps // reps)
+    head = measure_stack(torch, syn, ext, steps_per_rep, reps)
+    us = head["us_per_token"]
+    gbps = head["bytes"] / (us * 1e-6) / 1e9
+    line = {
+        "metric": "24-layer Qwen MoE stack µs/token + achieved HBM GB/s (% peak), batch 1",
+        "value": round(us, 3),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": head["steps"],
+        "warmup": 4,
+        "ms_per_step": round(us / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 / w8a16 (bf16 activations, fp32 accumulate)",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) token)",
+        "config": {
+            "workload": ("c3_qwen_stack: 24 x (RMSNorm + MoE block: router + top-4 of 60 experts I=1408 + bf16 shared "
+                         "expert 5632), routed BF16 in layers 0-15 and Q8 in 16-23, H=2048, one token, "
+                         f"{steps_per_rep} chained decode steps per timing"),
+            "tokens": 1,
+            "parallelism": "single GPU",
+        },
+        "us_per_layer": round(us / syn.C3_LAYERS, 3),
+        "multi_kernel_us_per_token": round(head["multi_kernel_us_per_token"], 3),
+        "algorithmic_bytes_per_token": int(head["bytes"]),
+        "hbm_gbps": round(gbps, 1),
+        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_stack(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def workload_name(shape) -> str:
     enc = {"q4_group128": "Q4", "q8_group128": "Q8", "bf16_le": "BF16"}[shape.encoding]
     w = (f"{shape.name}: one MoE block (router + top-{shape.top_k} of {shape.num_experts} {enc} experts "
@@ -263,6 +414,8 @@ def main() -> int:
     from uma_qmoe_amd.native_backend import load_native_extension
 
     _platform, ext = load_native_extension()
+    if args.config == "c3":
+        return main_stack(args, torch, syn, ext)
     shape = syn.CONFIGS[args.config]
     tokens = args.tokens if args.tokens > 0 else shape.tokens
     head = measure(torch, syn, ext, shape, tokens, args.steps, args.warmup, args.rotate_bytes)

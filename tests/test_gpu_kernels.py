@@ -299,3 +299,35 @@ def test_c3_stack_layer_encodings(hip_ext, layer_index):
            "shared_expert_gate": dense_c.shared_expert_gate}
     ref, *_ = om.qwen_block(x, lay, reader, layer_index, routes=(weights.cpu(), indices.cpu()))
     assert_close(out, ref, f"c3 layer {layer_index}")
+
+
+def test_c3_stack_chain(hip_ext):
+    """c3 stack driver: x <- MoE_l(RMSNorm(x)) chained on the device through
+    BF16 layers 0 and 15 and Q8 layers 16 and 23 for two decode steps. Every
+    layer is checked against the oracle given the same device input and the
+    device's routes (a free-running bf16 chain drifts by the rounding of every
+    layer, which a fixed tolerance cannot tell from a defect)."""
+    layer_ids = (0, 15, 16, 23)
+    parts = {}
+    for l in layer_ids:
+        shape = syn.c3_layer_shape(l)
+        layer = syn.build_experts(shape, layer=l, device=DEV)
+        dense = syn.build_dense(shape, layer=l, device=DEV)
+        dense_c = DenseBlock(*(None if v is None else v.cpu() for v in (
+            dense.router, dense.shared_gate, dense.shared_up, dense.shared_down, dense.shared_expert_gate)))
+        lay = {"router": dense_c.router, "top_k": shape.top_k, "num_experts": shape.num_experts,
+               "shared_gate": dense_c.shared_gate, "shared_up": dense_c.shared_up,
+               "shared_down": dense_c.shared_down, "shared_expert_gate": dense_c.shared_expert_gate}
+        parts[l] = (shape, layer, dense, lay, syn.DeviceLayerReader({l: layer}))
+    x_g = syn.hidden_states(syn.c3_layer_shape(0), 1, tag="c3_chain").to(DEV)
+    for step in range(2):
+        for l in layer_ids:
+            shape, layer, dense, lay, reader = parts[l]
+            note(f"c3 chain step {step} layer {l} {shape.encoding}")
+            x_in = x_g.cpu()
+            n_g = hip_ext.rmsnorm(x_g, 1e-6)
+            n_o = om.rmsnorm(x_in, 1e-6)
+            assert ((n_g.cpu().float() - n_o.float()).abs() <= n_o.float().abs() * 2.0 ** -7 + 1e-30).all()
+            x_g, _, weights, indices = hip_ext.moe_layer(layer, dense, n_g, shape.top_k)
+            ref, *_ = om.qwen_block(n_g.cpu(), lay, reader, l, routes=(weights.cpu(), indices.cpu()))
+            assert_close(x_g, ref, f"c3 chain step {step} layer {l}")

@@ -352,7 +352,11 @@ int run_shared(const uqm_layer_weights* layer, const uint16_t* x, int64_t T, int
   const int64_t Is = layer->shared_intermediate_size;
   *parts = 1;
   if (shared_uses_mfma(H, Is, T)) {
-    const int nb = nb_for(UQM_BF16, static_cast<double>(T));
+    // Up to 32 tokens: 16-token tiles, so that the plan can split K over
+    // waves (16-row items) and fill the grid; the second tile of a row block
+    // runs right after the first on the same workgroup and reads the rows
+    // from L2.
+    const int nb = T <= 32 ? 1 : nb_for(UQM_BF16, static_cast<double>(T));
     const int ntok = 16 * nb;
     const int64_t tiles = (T + ntok - 1) / ntok;
     const int cus = device_cus();

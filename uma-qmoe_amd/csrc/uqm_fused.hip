@@ -637,18 +637,31 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     int jj, s, c;
     bool ok;
   };
-  int jjs_[NJ], js_[NJ];  // job index (0 past the end) and slot; -1 slot past the end
-#pragma unroll
-  for (int t = 0; t < NJ; ++t) {
+  // Up to 4 jobs per lane their index and slot are kept in registers; with
+  // more (Q8/BF16 rows) they are recomputed at each use (a few VALU ops).
+  constexpr bool kJobRegs = NJ <= 4;
+  int jjs_[kJobRegs ? NJ : 1], js_[kJobRegs ? NJ : 1];  // job index (0 past the end); slot, -1 past the end
+  auto job_slot = [&](int t, int& jj, int& sl) {
     const int j = lane + 64 * t;
-    jjs_[t] = j < jobs ? j : 0;
-    js_[t] = j < jobs ? static_cast<int>((static_cast<float>(jjs_[t]) + 0.5f) * rcp_cr) : -1;
+    jj = j < jobs ? j : 0;
+    sl = j < jobs ? static_cast<int>((static_cast<float>(jj) + 0.5f) * rcp_cr) : -1;
+  };
+  if constexpr (kJobRegs) {
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) job_slot(t, jjs_[t], js_[t]);
   }
   auto job = [&](int t) {
+    int jj, sl;
+    if constexpr (kJobRegs) {
+      jj = jjs_[t];
+      sl = js_[t];
+    } else {
+      job_slot(t, jj, sl);
+    }
     Job r;
-    r.ok = js_[t] >= 0;
-    r.jj = jjs_[t];
-    r.s = r.ok ? js_[t] : 0;
+    r.ok = sl >= 0;
+    r.jj = jj;
+    r.s = r.ok ? sl : 0;
     r.c = r.jj - r.s * CR;
     return r;
   };
@@ -736,16 +749,22 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   const uint64_t* hr64 = reinterpret_cast<const uint64_t*>(a.hr);
   const int n2s = Is / 2, n2r = k * I / 2;
   const int base0 = wave * 64 + lane;
-  uint64_t vs[SL];
-  if constexpr (kShared) load_round(hs64, n2s, base0, vs);
-  issue_cr(oa < ob ? oa : H - 1);
-  issue_cs(oa < ob ? oa : H - 1, colIS);
-  if constexpr (kShared) {
+  // Rows wider than Q4 (Q8/BF16 routed down rows) do not fit in registers
+  // beside the shared down row: there the routed down rows are issued once
+  // the shared part is reduced.
+  auto stage_hs = [&](uint64_t (&vs)[SL]) {
     finish_round(hs64, n2s, base0, reinterpret_cast<uint32_t*>(lhs), vs);
     for (int b2 = base0 + kRound; b2 - lane < n2s; b2 += kRound) {
       load_round(hs64, n2s, b2, vs);
       finish_round(hs64, n2s, b2, reinterpret_cast<uint32_t*>(lhs), vs);
     }
+  };
+  {
+    uint64_t vs[SL];
+    if constexpr (kShared) load_round(hs64, n2s, base0, vs);
+    if constexpr (kJobRegs || !kShared) issue_cr(oa < ob ? oa : H - 1);
+    issue_cs(oa < ob ? oa : H - 1, colIS);
+    if constexpr (kShared) stage_hs(vs);
   }
   uint64_t vr[SL];
   load_round(hr64, n2r, base0, vr);
@@ -790,6 +809,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     return acc;
   };
   const float acc_s = shared_part(colIS);
+  if constexpr (!kJobRegs && kShared) issue_cr(oa < ob ? oa : H - 1);
   finish_round(hr64, n2r, base0, reinterpret_cast<uint32_t*>(lhr), vr);
   for (int b2 = base0 + kRound; b2 - lane < n2r; b2 += kRound) {
     load_round(hr64, n2r, b2, vr);
@@ -844,10 +864,9 @@ int fused_config_id(int enc, int64_t H, int64_t I, int64_t Is, int64_t k, int64_
   const int el = enc == kQ4 ? 32 : enc == kQ8 ? 16 : 8;
   const int ch = cpl(H / 8), chr = cpl(H / el), cir = cpl(I / el), cis = Is > 0 ? cpl(Is / 8) : 0;
   if (k < 1 || k > 8 || k > E || E < 1 || E + 1 > 320 || ch > 4 || cis > 11) return -1;
-  // Instantiations whose rows all fit in registers (others run the
-  // multi-kernel path): Q4 with a shared expert and k <= 4 or without one and
-  // k <= 8; Q8 and BF16 without a shared expert and k <= 4.
-  if (enc == kQ4 ? (Is > 0 && k > 4) : (Is > 0 || k > 4)) return -1;
+  // Instantiations (others run the multi-kernel path): Q4 with a shared
+  // expert and k <= 4 or without one and k <= 8; Q8 and BF16 with k <= 4.
+  if (k > (enc == kQ4 && Is == 0 ? 8 : 4)) return -1;
   if (H % 8 != 0 || I % 8 != 0 || Is % 8 != 0) return -1;
   const size_t lds = enc == kQ4 ? fused_lds_bytes<kQ4>(I, Is, k)
                                  : enc == kQ8 ? fused_lds_bytes<kQ8>(I, Is, k) : fused_lds_bytes<kBF16>(I, Is, k);
@@ -865,8 +884,9 @@ hipError_t launch_moe_decode_fused(int enc, const FusedArgs& a, hipStream_t stre
     if (a.Is > 0) return launch_cfg<kQ4, 4, 1, 1, 11, 4>(a, stream);
     return k4 ? launch_cfg<kQ4, 4, 1, 1, 0, 4>(a, stream) : launch_cfg<kQ4, 4, 1, 1, 0, 8>(a, stream);
   }
-  if (enc == kQ8) return launch_cfg<kQ8, 4, 2, 2, 0, 4>(a, stream);
-  return launch_cfg<kBF16, 4, 4, 3, 0, 4>(a, stream);
+  const bool shared = a.Is > 0;
+  if (enc == kQ8) return shared ? launch_cfg<kQ8, 4, 2, 2, 11, 4>(a, stream) : launch_cfg<kQ8, 4, 2, 2, 0, 4>(a, stream);
+  return shared ? launch_cfg<kBF16, 4, 4, 3, 11, 4>(a, stream) : launch_cfg<kBF16, 4, 4, 3, 0, 4>(a, stream);
 }
 
 }  // namespace uqm
