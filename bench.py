@@ -235,11 +235,12 @@ def measure_stack(torch, syn, ext, steps_per_rep: int, reps: int):
     """c3: the 24-layer Qwen stack, one token, ``steps_per_rep`` decode steps
     of x <- MoE_l(RMSNorm(x)) for l = 0..23 (routed BF16 in layers 0-15, Q8 in
     16-23, BF16 shared expert in every layer; RMSNorm eps 1e-6, weight ones).
-    One step (24 norms + 24 blocks) is captured in a HIP graph that reads and
-    writes the same token buffer, so replays chain the steps. The ~22.6 GB of
-    weights are read once per step (no MALL reuse). Returns the median over
-    ``reps`` of the per-step time, for the fused single-token kernel and for
-    the multi-kernel path."""
+    One step (24 pre-normalised blocks) is captured in a HIP graph that starts
+    and ends in the same token buffer, so replays chain the steps. The ~22.6 GB
+    of weights are read once per step (no MALL reuse). Returns the median over
+    ``reps`` of the per-step time for: the fused single-token kernel with the
+    norm folded in (the product path), the same kernel after a separate
+    RMSNorm launch, and the multi-kernel path."""
     from uma_qmoe_amd import _native
 
     dev = torch.device("cuda:0")
@@ -249,20 +250,26 @@ def measure_stack(torch, syn, ext, steps_per_rep: int, reps: int):
     s0 = shapes[0]
     ws = ext._workspace(dev, 1, s0.hidden, s0.intermediate, s0.shared_intermediate, s0.num_experts, s0.top_k)
     x0 = syn.hidden_states(s0, 1, device=dev, tag="c3_x0")
-    xbuf = x0.clone()
+    # layer l reads bufs[l % 2] and writes bufs[(l + 1) % 2]: an even layer
+    # count ends every step in bufs[0], where the next step starts
+    bufs = [x0.clone(), torch.empty_like(x0)]
     # one token routes to top_k distinct experts in every layer
     algo = sum(syn.algorithmic_bytes(layers[l], denses[l], s.top_k) for l, s in enumerate(shapes))
 
-    def step():
+    def step_folded():
         for l, s in enumerate(shapes):
-            normed = ext.rmsnorm(xbuf, 1e-6)
-            res = ext.moe_layer(layers[l], denses[l], normed, s.top_k, out=xbuf, workspace=ws)
-        return res
+            ext.norm_moe_layer(layers[l], denses[l], bufs[l % 2], s.top_k, 1e-6, out=bufs[(l + 1) % 2], workspace=ws)
+
+    def step_separate():
+        for l, s in enumerate(shapes):
+            normed = ext.rmsnorm(bufs[l % 2], 1e-6)
+            ext.moe_layer(layers[l], denses[l], normed, s.top_k, out=bufs[(l + 1) % 2], workspace=ws)
 
     out = {}
-    for mode, fused in (("fused", 1), ("multi_kernel", 0)):
+    for mode, fused, step in (("fused", 1, step_folded), ("fused_separate_norm", 1, step_separate),
+                              ("multi_kernel", 0, step_folded)):
         ext.set_option(_native.UQM_OPT_FUSED_DECODE, fused)
-        xbuf.copy_(x0)
+        bufs[0].copy_(x0)
         for _ in range(2):
             step()
         torch.cuda.synchronize()
@@ -283,15 +290,15 @@ def measure_stack(torch, syn, ext, steps_per_rep: int, reps: int):
             torch.cuda.synchronize()
             samples.append(start.elapsed_time(stop) * 1000.0 / steps_per_rep)
         ext.workspace_status(ws)
-        if not bool(torch.isfinite(xbuf.float()).all()):
+        if not bool(torch.isfinite(bufs[0].float()).all()):
             raise RuntimeError(f"c3 stack ({mode}) produced non-finite values")
         out[mode] = sorted(samples)[len(samples) // 2]
         del graph
     ext.set_option(_native.UQM_OPT_FUSED_DECODE, 1)
     del layers, denses, ws
     torch.cuda.empty_cache()
-    return {"us_per_token": out["fused"], "multi_kernel_us_per_token": out["multi_kernel"], "bytes": algo,
-            "steps": steps_per_rep * reps}
+    return {"us_per_token": out["fused"], "separate_norm_us_per_token": out["fused_separate_norm"],
+            "multi_kernel_us_per_token": out["multi_kernel"], "bytes": algo, "steps": steps_per_rep * reps}
 
 
 def cpu_baseline_stack(seconds: float):
@@ -368,6 +375,7 @@ def main_stack(args, torch, syn, ext) -> int:
             "parallelism": "single GPU",
         },
         "us_per_layer": round(us / syn.C3_LAYERS, 3),
+        "separate_norm_us_per_token": round(head["separate_norm_us_per_token"], 3),
         "multi_kernel_us_per_token": round(head["multi_kernel_us_per_token"], 3),
         "algorithmic_bytes_per_token": int(head["bytes"]),
         "hbm_gbps": round(gbps, 1),

@@ -162,6 +162,20 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
                   void* routing_weights, int64_t* expert_indices, void* workspace, size_t workspace_bytes,
                   void* stream);
 
+/* Pre-normalised block, as a decoder layer calls it:
+ *   out = MoE(RMSNorm(hidden)),  RMSNorm(x) = bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))
+ * (Transformers Qwen2MoeRMSNorm, modeling_qwen2_moe.py:65-70, the
+ * post_attention_layernorm that Qwen2MoeDecoderLayer applies before the block
+ * the reference replaces, src/uma_qmoe/qwen_compressed_loader.py:67-86).
+ * norm_weight bf16 [H] or NULL for ones; eps >= 0; output must not overlap
+ * hidden. Otherwise as uqm_moe_layer;
+ * on the single-token fused path the norm is folded into the kernel's
+ * activation staging (no extra launch), elsewhere it is one launch into the
+ * workspace. */
+int uqm_norm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, const void* norm_weight,
+                       float eps, void* output, void* logits, void* routing_weights, int64_t* expert_indices,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* Sets a process-wide option (UQM_OPT_*). No counterpart in the reference:
  * it selects between this library's own single-token code paths. */
 int uqm_set_option(int option, int64_t value);

@@ -22,7 +22,7 @@ import torch
 from golden.make_golden import weights_digest
 from golden_cases import load, regenerate
 from oracle import moe as om
-from test_gpu_kernels import DEV, assert_close, dense_to_dev, note, to_dev
+from test_gpu_kernels import DEV, assert_close, dense_to_cpu, dense_to_dev, note, to_dev
 from uma_qmoe_amd import _native
 from uma_qmoe_amd import synthetic as syn
 
@@ -118,3 +118,52 @@ def test_fused_topk_variants_match_oracle(fused_default, k, norm, enc):
     lay = {"router": dense.router, "top_k": k, "num_experts": shape.num_experts, "norm_topk_prob": norm}
     ref, *_ = om.olmoe_block(x, lay, syn.DeviceLayerReader({0: layer}), 0, routes=(weights, indices))
     assert_close(out, ref, f"fused k={k}")
+
+
+def _norm_case(case):
+    if case == "c1":
+        return syn.C1, 0
+    if case == "c2":
+        return syn.C2, 0
+    layer_index = int(case.split("_l")[1])
+    return syn.c3_layer_shape(layer_index), layer_index
+
+
+@pytest.mark.parametrize("tokens", [1, 3])
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("case", ["c1", "c2", "c3_l0", "c3_l16"])
+@pytest.mark.parametrize("fused", [1, 0])
+def test_norm_block_matches_oracle(fused_default, case, weighted, tokens, fused):
+    """MoE(RMSNorm(x)) in one call (folded into the fused kernel's activation
+    staging for one token) against the oracle's RMSNorm followed by its block,
+    given the device's routes."""
+    hip_ext = fused_default
+    if tokens > 1 and fused == 0:
+        pytest.skip("multi-token calls never take the fused path: covered by fused=1")
+    note(f"norm block {case} weighted={weighted} tokens={tokens} fused={fused}")
+    hip_ext.set_option(_native.UQM_OPT_FUSED_DECODE, fused)
+    shape, layer_index = _norm_case(case)
+    layer = syn.build_experts(shape, layer=layer_index, device=DEV)
+    dense = syn.build_dense(shape, layer=layer_index, device=DEV)
+    # a residual stream is far from unit RMS: scale it, so a missing norm shows
+    x = (syn.hidden_states(shape, tokens, tag="norm").float() * 7.5).to(torch.bfloat16)
+    w = None
+    if weighted:
+        w = (1.0 + syn.normal((shape.hidden,), seed=5, std=0.25)).to(torch.bfloat16)
+    out, logits, weights, indices = hip_ext.norm_moe_layer(layer, dense, x.to(DEV), shape.top_k, 1e-6,
+                                                           None if w is None else w.to(DEV))
+    torch.cuda.synchronize()
+    out, logits, weights, indices = out.cpu(), logits.cpu(), weights.cpu(), indices.cpu()
+    xn = om.rmsnorm(x, 1e-6, w)
+    dense_c = dense_to_cpu(dense)
+    ref_logits = torch.nn.functional.linear(xn, dense_c.router).float()
+    # the device's sum of squares may round differently, moving a normalised
+    # element by one bf16 ulp: its effect on a logit is far below 2^-12
+    assert bool(((logits.float() - ref_logits).abs() <= ref_logits.abs() * 2.0 ** -7 + 2.0 ** -12).all())
+    assert torch.equal(indices, om.topk_ordered(logits, shape.top_k))
+    lay = {"router": dense_c.router, "top_k": shape.top_k, "num_experts": shape.num_experts,
+           "shared_gate": dense_c.shared_gate, "shared_up": dense_c.shared_up, "shared_down": dense_c.shared_down,
+           "shared_expert_gate": dense_c.shared_expert_gate}
+    ref, *_ = om.qwen_block(xn, lay, syn.DeviceLayerReader({layer_index: layer}), layer_index,
+                            routes=(weights, indices))
+    assert_close(out, ref, f"norm block {case} weighted={weighted} tokens={tokens} fused={fused}")

@@ -42,6 +42,11 @@ def dense_to_dev(d: DenseBlock) -> DenseBlock:
     return DenseBlock(mv(d.router), mv(d.shared_gate), mv(d.shared_up), mv(d.shared_down), mv(d.shared_expert_gate))
 
 
+def dense_to_cpu(d: DenseBlock) -> DenseBlock:
+    mv = lambda t: None if t is None else t.cpu()
+    return DenseBlock(mv(d.router), mv(d.shared_gate), mv(d.shared_up), mv(d.shared_down), mv(d.shared_expert_gate))
+
+
 def assert_close(got: torch.Tensor, ref: torch.Tensor, what: str, rel=REL_L2, mx=MAX_ABS):
     r = om.rel_l2(got.cpu(), ref.cpu())
     m = om.max_abs(got.cpu(), ref.cpu())

@@ -41,7 +41,7 @@ size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 constexpr int kMaxSplit = 4;
 
 struct Layout {
-  size_t fused_sync, fused_hs, fused_hr, fused_lgt, counters, route_expert, route_order, expert_offsets, active_experts,
+  size_t fused_sync, fused_hs, fused_hr, fused_lgt, normed, counters, route_expert, route_order, expert_offsets, active_experts,
       tiles, logits, weights, indices, sg, router_part, h_routed, y_routed, h_shared, y_shared, total;
 };
 
@@ -58,6 +58,7 @@ Layout layout(int64_t T, int64_t H, int64_t I, int64_t Is, int64_t E, int64_t k)
   L.fused_hs = take(4 * static_cast<size_t>(Is));
   L.fused_hr = take(4 * static_cast<size_t>(k) * I);
   L.fused_lgt = take(8 * static_cast<size_t>(E + 1));
+  L.normed = take(2 * static_cast<size_t>(T) * H);  // RMSNorm(hidden) of a pre-normalised block
   L.counters = take(256);
   L.route_expert = take(4 * R);
   L.route_order = take(4 * R);
@@ -586,9 +587,18 @@ int uqm_moe_forward(const uqm_expert_weights* weights, const void* hidden, int64
                    "combine launch");
 }
 
-int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, void* output, void* logits,
-                  void* routing_weights, int64_t* expert_indices, void* workspace, size_t workspace_bytes,
-                  void* stream) {
+namespace {
+
+// RMSNorm applied to the block's input (rms == false: none).
+struct InputNorm {
+  bool rms;
+  const void* weight;
+  float eps;
+};
+
+int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, InputNorm norm, void* output,
+                   void* logits, void* routing_weights, int64_t* expert_indices, void* workspace,
+                   size_t workspace_bytes, void* stream) {
   using namespace uqm;
   int rc = check_device();
   if (rc) return rc;
@@ -617,6 +627,9 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
   if (workspace == nullptr || workspace_bytes < L.total || !aligned16(workspace))
     return fail(UQM_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required (or misaligned)",
                 workspace_bytes, L.total);
+  if (norm.rms && !(norm.eps >= 0.f)) return fail(UQM_ERR_ARGUMENT, "RMSNorm eps must be >= 0");
+  if (norm.rms && norm.weight != nullptr && !aligned16(norm.weight))
+    return fail(UQM_ERR_ARGUMENT, "RMSNorm weight must be a 16-byte aligned device pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* x = static_cast<const uint16_t*>(hidden);
   const int nt = static_cast<int>(tokens < 4 ? tokens : 4);
@@ -628,6 +641,9 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
       (w->encoding == UQM_BF16 || (H % w->group_size == 0 && w->intermediate_size % w->group_size == 0))) {
     FusedArgs fa{};
     fa.x = x;
+    fa.rms = norm.rms ? 1 : 0;
+    fa.rms_w = static_cast<const uint16_t*>(norm.weight);
+    fa.rms_eps = norm.eps;
     fa.router = static_cast<const uint8_t*>(layer->router);
     fa.shared_expert_gate = static_cast<const uint8_t*>(layer->shared_expert_gate);
     fa.sg_w = static_cast<const uint8_t*>(layer->shared_gate);
@@ -657,6 +673,14 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
     return hip_check(launch_moe_decode_fused(w->encoding, fa, s), "fused block launch");
   }
 
+  // 0. input RMSNorm into the workspace
+  if (norm.rms) {
+    uint16_t* xn = at<uint16_t>(workspace, L.normed);
+    if ((rc = hip_check(launch_rmsnorm(x, tokens, H, static_cast<const uint16_t*>(norm.weight), norm.eps, xn, s),
+                        "rmsnorm launch")))
+      return rc;
+    x = xn;
+  }
   // 1-2. router logits (+ shared-gate logit in column E), top-k
   uint16_t* wout = routing_weights != nullptr ? static_cast<uint16_t*>(routing_weights) : at<uint16_t>(workspace, L.weights);
   int64_t* iout = expert_indices != nullptr ? expert_indices : at<int64_t>(workspace, L.indices);
@@ -712,6 +736,22 @@ int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t to
                                   H, layer->has_shared ? at<float>(workspace, L.y_shared) : nullptr, ys_parts,
                                   tokens * H, sg, static_cast<uint16_t*>(output), s),
                    "combine launch");
+}
+
+}  // namespace
+
+int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, void* output, void* logits,
+                  void* routing_weights, int64_t* expert_indices, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  return moe_layer_impl(layer, hidden, tokens, InputNorm{false, nullptr, 0.f}, output, logits, routing_weights,
+                        expert_indices, workspace, workspace_bytes, stream);
+}
+
+int uqm_norm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, const void* norm_weight,
+                       float eps, void* output, void* logits, void* routing_weights, int64_t* expert_indices,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  return moe_layer_impl(layer, hidden, tokens, InputNorm{true, norm_weight, eps}, output, logits, routing_weights,
+                        expert_indices, workspace, workspace_bytes, stream);
 }
 
 int uqm_set_option(int option, int64_t value) {

@@ -204,6 +204,61 @@ __device__ __forceinline__ void frags_from(const uint16_t* row, const Cols<ENC, 
   frags_of<ENC, CPL>(r, f);
 }
 
+// Input RMSNorm folded into the activation staging (Transformers
+// Qwen2MoeRMSNorm, modeling_qwen2_moe.py:65-70):
+//   x' = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), w = 1 without a weight.
+// The FP32 sum of squares is taken over the row in the 8-element chunk layout
+// (chunk lane + 64 j) in one fixed order, so that every wave of every
+// workgroup derives the same scale whatever layout it stages x in.
+template <int CPL>
+__device__ __forceinline__ float rms_scale(const XRaw<kBF16, CPL>& r, const Cols<kBF16, CPL>& cl, int64_t H,
+                                           float eps) {
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    float sj = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float lo = __uint_as_float(r.w[j][q] << 16), hi = __uint_as_float(r.w[j][q] & 0xFFFF0000u);
+      sj = fmaf(lo, lo, sj);
+      sj = fmaf(hi, hi, sj);
+    }
+    s += cl.m(j) * sj;
+  }
+  return rsqrtf(wave_sum(s) / static_cast<float>(H) + eps);
+}
+
+template <int ENC, int CPL, bool kWeight>
+__device__ __forceinline__ void rms_apply(XRaw<ENC, CPL>& r, float scale, const XRaw<ENC, CPL>& w) {
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+    for (int q = 0; q < Enc<ENC>::kElems / 2; ++q) {
+      const uint32_t v = r.w[j][q];
+      float lo = round_bf16(__uint_as_float(v << 16) * scale), hi = round_bf16(__uint_as_float(v & 0xFFFF0000u) * scale);
+      if constexpr (kWeight) {
+        lo *= __uint_as_float(w.w[j][q] << 16);
+        hi *= __uint_as_float(w.w[j][q] & 0xFFFF0000u);
+      }
+      r.w[j][q] = static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+    }
+  }
+}
+
+// Normalises the staged row `r` (layout cl) with `scale`, reading the weight
+// row in the same layout when there is one.
+template <int ENC, int CPL>
+__device__ __forceinline__ void rms_normalise(XRaw<ENC, CPL>& r, const Cols<ENC, CPL>& cl, float scale,
+                                              const uint16_t* weight) {
+  if (weight != nullptr) {
+    XRaw<ENC, CPL> w;
+    load_x<ENC, CPL>(weight, cl, w);
+    rms_apply<ENC, CPL, true>(r, scale, w);
+  } else {
+    rms_apply<ENC, CPL, false>(r, scale, r);
+  }
+}
+
 // One matrix row's 16-byte chunks at this lane's columns, plus their scales.
 template <int ENC, int CPL>
 struct RowLoad {
@@ -300,7 +355,7 @@ size_t fused_lds_bytes(int64_t I, int64_t Is, int64_t k) {
 // Template parameters: routed encoding; 16-byte chunks per lane for a BF16
 // row of H (CH), an encoded row of H (CHR), an encoded row of I (CIR) and a
 // BF16 row of Is (CIS, 0 without a shared expert); KMAX >= top_k.
-template <int ENC, int CH, int CHR, int CIR, int CIS, int KMAX>
+template <int ENC, int CH, int CHR, int CIR, int CIS, int KMAX, bool RMS>
 __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a) {
   using ER = Enc<ENC>;
   constexpr int CISX = CIS > 0 ? CIS : 1;  // array extent when there is no shared expert
@@ -395,9 +450,16 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     XRaw<kBF16, CH> x_raw;
     load_x<kBF16, CH>(a.x, colH16, x_raw);
     const uint32_t last_epoch = co_load(my_epoch + opaque_zero());
+    bool normed = false;
     for (int r = b; r < nrow; r += nb) {
       RowLoad<kBF16, CH> rl;
       issue_row<kBF16, CH>(r < E ? a.router + r * rowH16 : a.shared_expert_gate, nullptr, colH16, rl);
+      if constexpr (RMS) {
+        if (!normed) {  // after the first row is issued: the norm waits for x only
+          rms_normalise<kBF16, CH>(x_raw, colH16, rms_scale<CH>(x_raw, colH16, H, a.rms_eps), a.rms_w);
+          normed = true;
+        }
+      }
       XFrag<kBF16> xb[CH];
       frags_of<kBF16, CH>(x_raw, xb);
       const float g = wave_sum(dot_row<kBF16, CH>(rl, xb, colH16));
@@ -543,10 +605,15 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   // Activation words and the epoch first: waits for them then never wait for
   // weight rows issued later.
   XRaw<kBF16, CH> xb_raw;
-  if constexpr (kShared) load_x<kBF16, CH>(a.x, colH16, xb_raw);
+  if constexpr (kShared || RMS) load_x<kBF16, CH>(a.x, colH16, xb_raw);
   XRaw<ENC, CHR> xr_raw;
   load_x<ENC, CHR>(a.x, colHR, xr_raw);
   const uint32_t last_epoch = co_load(my_epoch + opaque_zero());
+  if constexpr (RMS) {
+    const float scale = rms_scale<CH>(xb_raw, colH16, H, a.rms_eps);
+    if constexpr (kShared) rms_normalise<kBF16, CH>(xb_raw, colH16, scale, a.rms_w);
+    rms_normalise<ENC, CHR>(xr_raw, colHR, scale, a.rms_w);
+  }
   // The epoch is derived from last_epoch where each product is stored, after
   // that product's dot (see pinned_after).
   auto epoch_after = [&](float dep) { return next_epoch(pinned_after(last_epoch, dep)); };
@@ -839,10 +906,9 @@ namespace {
 
 int cpl(int64_t chunks) { return static_cast<int>((chunks + 63) / 64); }
 
-
-template <int ENC, int CH, int CHR, int CIR, int CIS, int KMAX>
-hipError_t launch_cfg(const FusedArgs& args, hipStream_t stream) {
-  auto kern = moe_decode_fused_kernel<ENC, CH, CHR, CIR, CIS, KMAX>;
+template <int ENC, int CH, int CHR, int CIR, int CIS, int KMAX, bool RMS>
+hipError_t launch_kernel(const FusedArgs& args, hipStream_t stream) {
+  auto kern = moe_decode_fused_kernel<ENC, CH, CHR, CIR, CIS, KMAX, RMS>;
   const size_t lds = fused_lds_bytes<ENC>(args.I, args.Is, args.k);
   if (lds > 64 * 1024) return hipErrorInvalidValue;
   int dev = 0;
@@ -876,6 +942,18 @@ int fused_config_id(int enc, int64_t H, int64_t I, int64_t Is, int64_t k, int64_
   if (enc == kBF16 && chr <= 4 && cir <= 3) return 2;
   return -1;
 }
+
+namespace {
+
+// The input norm is a template parameter: the kernels without it are not
+// perturbed by its code (register allocation, scheduling).
+template <int ENC, int CH, int CHR, int CIR, int CIS, int KMAX>
+hipError_t launch_cfg(const FusedArgs& args, hipStream_t stream) {
+  return args.rms ? launch_kernel<ENC, CH, CHR, CIR, CIS, KMAX, true>(args, stream)
+                  : launch_kernel<ENC, CH, CHR, CIR, CIS, KMAX, false>(args, stream);
+}
+
+}  // namespace
 
 hipError_t launch_moe_decode_fused(int enc, const FusedArgs& a, hipStream_t stream) {
   if (fused_config_id(enc, a.H, a.I, a.Is, a.k, a.E) < 0) return hipErrorInvalidValue;

@@ -131,6 +131,9 @@ constexpr int kSyncWords = kSyncEpochBase + kMaxFusedBlocks;
 
 struct FusedArgs {
   const uint16_t* x;                   // [H] bf16, 16-byte aligned
+  const uint16_t* rms_w;               // [H] bf16 RMSNorm weight applied to x (NULL: ones)
+  float rms_eps;
+  int rms;                             // 1: the block's input is RMSNorm(x)
   const uint8_t* router;               // [E, H] bf16
   const uint8_t* shared_expert_gate;   // [H] bf16 (shared expert only)
   const uint8_t* sg_w;                 // shared gate [Is, H] bf16

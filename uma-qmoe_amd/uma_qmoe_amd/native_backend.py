@@ -282,6 +282,34 @@ class HipExtension:
         _native.check(rc, "uqm_moe_layer")
         return result.reshape(hidden.shape), logits, weights, indices
 
+    def norm_moe_layer(self, layer: DeviceExperts, dense: DenseBlock, hidden, top_k, eps=1e-6, norm_weight=None,
+                       norm_topk_prob=False, *, out=None, workspace=None):
+        """MoE block on RMSNorm(hidden) (eps, bf16 weight [H] or None for ones).
+        Returns (out, logits, weights, indices) like ``moe_layer``."""
+        torch = self.torch
+        self._check_hidden(hidden)
+        x = hidden.reshape(-1, layer.hidden_size).contiguous()
+        t = x.shape[0]
+        e = layer.num_experts
+        shared_i = int(dense.shared_gate.shape[0]) if dense.has_shared else 0
+        result = torch.empty_like(x) if out is None else out
+        logits = torch.empty((t, e), dtype=torch.bfloat16, device=x.device)
+        weights = torch.empty((t, top_k), dtype=torch.bfloat16, device=x.device)
+        indices = torch.empty((t, top_k), dtype=torch.int64, device=x.device)
+        ws = workspace
+        if ws is None:
+            ws = self._workspace(x.device, t, layer.hidden_size, layer.intermediate_size, shared_i, e, top_k)
+        if norm_weight is not None:
+            if norm_weight.dtype != torch.bfloat16 or norm_weight.numel() != layer.hidden_size:
+                raise RuntimeError("norm_weight must be bf16 [hidden_size]")
+            norm_weight = norm_weight.contiguous()
+        desc = self.layer_descriptor(layer, dense, top_k, norm_topk_prob)
+        rc = self.lib.uqm_norm_moe_layer(ctypes.byref(desc), _ptr(x), t, _ptr(norm_weight), float(eps), _ptr(result),
+                                         _ptr(logits), _ptr(weights), _ptr(indices), _ptr(ws), ws.numel(),
+                                         _stream_handle(torch, x.device))
+        _native.check(rc, "uqm_norm_moe_layer")
+        return result.reshape(hidden.shape), logits, weights, indices
+
     @staticmethod
     def layer_descriptor(layer: DeviceExperts, dense: DenseBlock, top_k: int, norm_topk_prob=False) -> _native.LayerWeights:
         shared_i = int(dense.shared_gate.shape[0]) if dense.has_shared else 0
