@@ -66,7 +66,8 @@ constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a wait gives up (well
 constexpr int kPollSleep = 40;             // s_sleep units (64 clocks) between router logit polls
 constexpr int kPollDelay = 64;             // s_sleep units before the first poll (the logits cannot be
                                            // in sooner; fewer polls leave more bandwidth to phase A)
-constexpr int kRouterHeadStart = 12;       // s_sleep units the streaming waves of router workgroups yield
+constexpr int kRouterHeadStart = 12;
+enum { kNormNone = 0, kNormUnit = 1, kNormWeighted = 2 };  // input RMSNorm: none, weight ones, weight row       // s_sleep units the streaming waves of router workgroups yield
 #ifndef UQM_FUSED_CTRL_PRIO
 #define UQM_FUSED_CTRL_PRIO 3
 #endif
@@ -228,34 +229,30 @@ __device__ __forceinline__ float rms_scale(const XRaw<kBF16, CPL>& r, const Cols
   return rsqrtf(wave_sum(s) / static_cast<float>(H) + eps);
 }
 
-template <int ENC, int CPL, bool kWeight>
-__device__ __forceinline__ void rms_apply(XRaw<ENC, CPL>& r, float scale, const XRaw<ENC, CPL>& w) {
+// A staged row normalised in place: x' = bf16(x * scale), then, with a
+// weight row w staged in the same layout, x' = bf16(w * x').
+template <int ENC, int CPL>
+__device__ __forceinline__ void rms_row(XRaw<ENC, CPL>& r, float scale) {
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
 #pragma unroll
     for (int q = 0; q < Enc<ENC>::kElems / 2; ++q) {
       const uint32_t v = r.w[j][q];
-      float lo = round_bf16(__uint_as_float(v << 16) * scale), hi = round_bf16(__uint_as_float(v & 0xFFFF0000u) * scale);
-      if constexpr (kWeight) {
-        lo *= __uint_as_float(w.w[j][q] << 16);
-        hi *= __uint_as_float(w.w[j][q] & 0xFFFF0000u);
-      }
-      r.w[j][q] = static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+      r.w[j][q] = pack_bf16x2(__uint_as_float(v << 16) * scale, __uint_as_float(v & 0xFFFF0000u) * scale);
     }
   }
 }
-
-// Normalises the staged row `r` (layout cl) with `scale`, reading the weight
-// row in the same layout when there is one.
 template <int ENC, int CPL>
-__device__ __forceinline__ void rms_normalise(XRaw<ENC, CPL>& r, const Cols<ENC, CPL>& cl, float scale,
-                                              const uint16_t* weight) {
-  if (weight != nullptr) {
-    XRaw<ENC, CPL> w;
-    load_x<ENC, CPL>(weight, cl, w);
-    rms_apply<ENC, CPL, true>(r, scale, w);
-  } else {
-    rms_apply<ENC, CPL, false>(r, scale, r);
+__device__ __forceinline__ void rms_row(XRaw<ENC, CPL>& r, float scale, const XRaw<ENC, CPL>& w) {
+  rms_row<ENC, CPL>(r, scale);
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+    for (int q = 0; q < Enc<ENC>::kElems / 2; ++q) {
+      const uint32_t n = r.w[j][q], m = w.w[j][q];
+      r.w[j][q] = pack_bf16x2(__uint_as_float(n << 16) * __uint_as_float(m << 16),
+                              __uint_as_float(n & 0xFFFF0000u) * __uint_as_float(m & 0xFFFF0000u));
+    }
   }
 }
 
@@ -355,9 +352,11 @@ size_t fused_lds_bytes(int64_t I, int64_t Is, int64_t k) {
 // Template parameters: routed encoding; 16-byte chunks per lane for a BF16
 // row of H (CH), an encoded row of H (CHR), an encoded row of I (CIR) and a
 // BF16 row of Is (CIS, 0 without a shared expert); KMAX >= top_k.
-template <int ENC, int CH, int CHR, int CIR, int CIS, int KMAX, bool RMS>
+template <int ENC, int CH, int CHR, int CIR, int CIS, int KMAX, int NORM>
 __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a) {
   using ER = Enc<ENC>;
+  constexpr bool RMS = NORM != kNormNone;         // the block's input is RMSNorm(x)
+  constexpr bool kWeighted = NORM == kNormWeighted;  // ... with a weight row (else ones)
   constexpr int CISX = CIS > 0 ? CIS : 1;  // array extent when there is no shared expert
   constexpr bool kShared = CIS > 0;
   // Routed gate+up row pairs per load batch (the most a wave takes at the
@@ -447,16 +446,21 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     // when it shares a SIMD with streaming waves.
     __builtin_amdgcn_s_setprio(UQM_FUSED_CTRL_PRIO);
     // Activation, epoch and router row loads go out together: one round trip.
-    XRaw<kBF16, CH> x_raw;
+    XRaw<kBF16, CH> x_raw, w_raw;
     load_x<kBF16, CH>(a.x, colH16, x_raw);
+    if constexpr (kWeighted) load_x<kBF16, CH>(a.rms_w, colH16, w_raw);
     const uint32_t last_epoch = co_load(my_epoch + opaque_zero());
-    bool normed = false;
+    bool normed = !RMS;
     for (int r = b; r < nrow; r += nb) {
       RowLoad<kBF16, CH> rl;
       issue_row<kBF16, CH>(r < E ? a.router + r * rowH16 : a.shared_expert_gate, nullptr, colH16, rl);
       if constexpr (RMS) {
-        if (!normed) {  // after the first row is issued: the norm waits for x only
-          rms_normalise<kBF16, CH>(x_raw, colH16, rms_scale<CH>(x_raw, colH16, H, a.rms_eps), a.rms_w);
+        if (!normed) {  // with the first row in flight
+          const float scale = rms_scale<CH>(x_raw, colH16, H, a.rms_eps);
+          if constexpr (kWeighted)
+            rms_row<kBF16, CH>(x_raw, scale, w_raw);
+          else
+            rms_row<kBF16, CH>(x_raw, scale);
           normed = true;
         }
       }
@@ -604,16 +608,30 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
 
   // Activation words and the epoch first: waits for them then never wait for
   // weight rows issued later.
-  XRaw<kBF16, CH> xb_raw;
+  XRaw<kBF16, CH> xb_raw, wb_raw;
   if constexpr (kShared || RMS) load_x<kBF16, CH>(a.x, colH16, xb_raw);
-  XRaw<ENC, CHR> xr_raw;
+  XRaw<ENC, CHR> xr_raw, wr_raw;
   load_x<ENC, CHR>(a.x, colHR, xr_raw);
-  const uint32_t last_epoch = co_load(my_epoch + opaque_zero());
-  if constexpr (RMS) {
-    const float scale = rms_scale<CH>(xb_raw, colH16, H, a.rms_eps);
-    if constexpr (kShared) rms_normalise<kBF16, CH>(xb_raw, colH16, scale, a.rms_w);
-    rms_normalise<ENC, CHR>(xr_raw, colHR, scale, a.rms_w);
+  if constexpr (kWeighted) {  // the norm's weight row in both layouts
+    if constexpr (kShared) load_x<kBF16, CH>(a.rms_w, colH16, wb_raw);
+    load_x<ENC, CHR>(a.rms_w, colHR, wr_raw);
   }
+  const uint32_t last_epoch = co_load(my_epoch + opaque_zero());
+  // Normalises the staged activations (the sum of squares is taken over the
+  // BF16 layout): done once the first weight rows are in flight, so that the
+  // arithmetic overlaps their loads.
+  auto normalise = [&]() {
+    if constexpr (RMS) {
+      const float scale = rms_scale<CH>(xb_raw, colH16, H, a.rms_eps);
+      if constexpr (kWeighted) {
+        if constexpr (kShared) rms_row<kBF16, CH>(xb_raw, scale, wb_raw);
+        rms_row<ENC, CHR>(xr_raw, scale, wr_raw);
+      } else {
+        if constexpr (kShared) rms_row<kBF16, CH>(xb_raw, scale);
+        rms_row<ENC, CHR>(xr_raw, scale);
+      }
+    }
+  };
   // The epoch is derived from last_epoch where each product is stored, after
   // that product's dot (see pinned_after).
   auto epoch_after = [&](float dep) { return next_epoch(pinned_after(last_epoch, dep)); };
@@ -624,17 +642,37 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   if constexpr (kShared) {
     const int pa = split_at(Is, sw, nsw), pb = split_at(Is, sw + 1, nsw);
     XFrag<kBF16> xb[CH];
-    frags_of<kBF16, CH>(xb_raw, xb);
-    for (int p = pa; p < pb; ++p) {
+    if constexpr (!RMS) frags_of<kBF16, CH>(xb_raw, xb);
+    auto pair = [&](int p, bool first) {
       RowLoad<kBF16, CH> rg, ru;
       issue_row<kBF16, CH>(a.sg_w + p * rowH16, nullptr, colH16, rg);
       issue_row<kBF16, CH>(a.su_w + p * rowH16, nullptr, colH16, ru);
+      if constexpr (RMS) {
+        if (first) {
+          normalise();
+          frags_of<kBF16, CH>(xb_raw, xb);
+        }
+      }
       float v[2] = {dot_row<kBF16, CH>(rg, xb, colH16), dot_row<kBF16, CH>(ru, xb, colH16)};
       const float sum = wave_multi_sum<2>(v);  // lanes 0-31: gate, 32-63: up
       const float up = xor_partner<32>(sum);
       if (lane == 0)
         co_store<uint32_t>(a.hs + p, tag16(epoch_after(sum), f32_to_bf16(silu(round_bf16(sum)) * round_bf16(up))));
+    };
+    if constexpr (RMS) {
+      // The first pair is peeled off, so that the norm's weight rows are dead
+      // in the loop.
+      if (pa < pb) {
+        pair(pa, true);
+        for (int p = pa + 1; p < pb; ++p) pair(p, false);
+      } else {
+        normalise();
+      }
+    } else {
+      for (int p = pa; p < pb; ++p) pair(p, false);
     }
+  } else {
+    normalise();
   }
   XFrag<ENC> xr[CHR];
   frags_of<ENC, CHR>(xr_raw, xr);
@@ -906,9 +944,9 @@ namespace {
 
 int cpl(int64_t chunks) { return static_cast<int>((chunks + 63) / 64); }
 
-template <int ENC, int CH, int CHR, int CIR, int CIS, int KMAX, bool RMS>
+template <int ENC, int CH, int CHR, int CIR, int CIS, int KMAX, int NORM>
 hipError_t launch_kernel(const FusedArgs& args, hipStream_t stream) {
-  auto kern = moe_decode_fused_kernel<ENC, CH, CHR, CIR, CIS, KMAX, RMS>;
+  auto kern = moe_decode_fused_kernel<ENC, CH, CHR, CIR, CIS, KMAX, NORM>;
   const size_t lds = fused_lds_bytes<ENC>(args.I, args.Is, args.k);
   if (lds > 64 * 1024) return hipErrorInvalidValue;
   int dev = 0;
@@ -945,12 +983,14 @@ int fused_config_id(int enc, int64_t H, int64_t I, int64_t Is, int64_t k, int64_
 
 namespace {
 
-// The input norm is a template parameter: the kernels without it are not
-// perturbed by its code (register allocation, scheduling).
+// The input norm is a template parameter: the kernels without it (or
+// without its weight row, which costs registers) are not perturbed by its
+// code (register allocation, scheduling).
 template <int ENC, int CH, int CHR, int CIR, int CIS, int KMAX>
 hipError_t launch_cfg(const FusedArgs& args, hipStream_t stream) {
-  return args.rms ? launch_kernel<ENC, CH, CHR, CIR, CIS, KMAX, true>(args, stream)
-                  : launch_kernel<ENC, CH, CHR, CIR, CIS, KMAX, false>(args, stream);
+  if (!args.rms) return launch_kernel<ENC, CH, CHR, CIR, CIS, KMAX, kNormNone>(args, stream);
+  return args.rms_w != nullptr ? launch_kernel<ENC, CH, CHR, CIR, CIS, KMAX, kNormWeighted>(args, stream)
+                               : launch_kernel<ENC, CH, CHR, CIR, CIS, KMAX, kNormUnit>(args, stream);
 }
 
 }  // namespace
