@@ -361,8 +361,9 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   constexpr bool kShared = CIS > 0;
   // Routed gate+up row pairs per load batch (the most a wave takes at the
   // shapes served: 5632 pairs / 2048 waves with a shared expert, 8192 / 2048
-  // without), and their value count rounded up to a power of two.
-  constexpr int RBP = CHR == 1 ? (kShared ? 3 : 4) : (CHR == 2 ? 2 : 1);
+  // without; BF16 rows, 4 KB each, two pairs), and their value count rounded
+  // up to a power of two. Each batch is one round trip.
+  constexpr int RBP = CHR == 1 ? (kShared ? 3 : 4) : (CHR == 2 ? 3 : 2);
   constexpr int VB = RBP == 3 ? 8 : 2 * RBP;
   // Routed down chunks per lane: the k rows of an output row are flattened
   // over the wave's lanes (k * CR chunks).
