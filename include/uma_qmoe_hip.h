@@ -15,8 +15,11 @@
  *     Q8: int8 codes + FP32 scales (src/uma_qmoe/target_pack.py:92-112).
  *     BF16: raw bf16 (src/uma_qmoe/target_pack.py:78-89).
  *     Nothing is ever dequantized to memory.
- *   - Kernels run on `stream` (pass torch's current stream). No entry point
- *     allocates device memory or synchronises (except uqm_workspace_status);
+ *   - Kernels run on `stream` (pass torch's current stream); multi-token
+ *     blocks with a shared expert fork it onto a library-owned side stream
+ *     and join it back with events (UQM_OPT_OVERLAP_SHARED). No entry point
+ *     allocates device memory or synchronises (except uqm_workspace_status;
+ *     the side stream and its two events are created once per device);
  *     temporaries live in the caller's `workspace`, sized by
  *     uqm_moe_workspace_bytes(). The workspace must be zero-filled before its
  *     first use: its first 4352 bytes hold the single-token fused kernel's
@@ -54,8 +57,12 @@ enum {
   UQM_OPT_FUSED_DECODE = 1,   /* 1 (default): single-token blocks use the fused persistent kernel */
   UQM_OPT_FUSED_ROUTED_BLOCKS = 2, /* accepted, no effect: every CU of the fused kernel takes a share
                                       of every phase (values 0..4096 as before) */
-  UQM_OPT_MFMA_MIN_TOKENS = 3      /* token count from which multi-token calls run the expert projections
+  UQM_OPT_MFMA_MIN_TOKENS = 3,     /* token count from which multi-token calls run the expert projections
                                       as MFMA grouped GEMMs (default 2; 0 = never, batched GEMV instead) */
+  UQM_OPT_OVERLAP_SHARED = 4       /* 1 (default): multi-token blocks run the shared expert on a
+                                      library-owned side stream (one per device, default priority),
+                                      forked from and joined back into the caller's stream with
+                                      events; 0: everything in order on the caller's stream */
 };
 
 /* Routed-expert weights of one MoE layer (device pointers). */

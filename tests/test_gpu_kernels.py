@@ -260,10 +260,16 @@ def test_moe_forward_benchmark_shapes(hip_ext, name, t):
     assert_close(got, ref, f"{shape.name} t={t}")
 
 
-@pytest.mark.parametrize("name,t", [("c2", 1), ("c1", 1), ("c2", 3)])
+# expert counts at which the shared-expert gate column (index E) of the router
+# output falls on lane 0 of the second and of the fifth 64-column slice
+GATE_COLUMN_SHAPES = {"e64_shared": syn.MoEShape("e64_shared", 256, 64, 2, 128, 128),
+                      "e256_shared": syn.MoEShape("e256_shared", 256, 256, 2, 128, 128)}
+
+
+@pytest.mark.parametrize("name,t", [("c2", 1), ("c1", 1), ("c2", 3), ("e64_shared", 3), ("e256_shared", 3)])
 def test_moe_layer_matches_oracle_block(hip_ext, name, t):
     """Whole block: router + routed + shared + sigmoid gate, one C-ABI call."""
-    shape = syn.CONFIGS[name]
+    shape = GATE_COLUMN_SHAPES[name] if name in GATE_COLUMN_SHAPES else syn.CONFIGS[name]
     note(f"moe_layer {shape.name} t={t}")
     layer = syn.build_experts(shape, device=DEV)
     dense = syn.build_dense(shape, device=DEV)

@@ -156,6 +156,43 @@ def test_qwen_block_batched_decode(mfma_on, t):
     close(out, out_g, f"c2 block mfma vs gemv t={t}", rel=5e-3, mx=1e-2)
 
 
+@pytest.mark.parametrize("t", [4, 32])
+def test_shared_expert_side_stream(mfma_on, t):
+    """The shared expert forked onto the library's side stream (the default)
+    gives the same bits as the in-order run on the caller's stream, eagerly and
+    replayed from a HIP graph (several replays, eager work in between)."""
+    ext = mfma_on
+    shape = syn.C2
+    note(f"shared expert side stream t={t}")
+    layer = syn.build_experts(shape, device=DEV)
+    dense = syn.build_dense(shape, device=DEV)
+    x = syn.hidden_states(shape, t, seed=70 + t).to(DEV)
+    ws = torch.zeros(ext.lib.uqm_moe_workspace_bytes(t, shape.hidden, shape.intermediate, shape.shared_intermediate,
+                                                     shape.num_experts, shape.top_k), dtype=torch.uint8, device=DEV)
+    try:
+        ext.set_option(_native.UQM_OPT_OVERLAP_SHARED, 0)
+        ref = [v.clone() for v in ext.moe_layer(layer, dense, x, shape.top_k, workspace=ws)]
+        ext.set_option(_native.UQM_OPT_OVERLAP_SHARED, 1)
+        got = ext.moe_layer(layer, dense, x, shape.top_k, workspace=ws)
+        for a, b, what in zip(got, ref, ("out", "logits", "weights", "indices")):
+            assert torch.equal(a, b), f"eager {what}"
+        out = torch.empty_like(x)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            ext.moe_layer(layer, dense, x, shape.top_k, out=out, workspace=ws)
+        for rep in range(3):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref[0]), f"graph replay {rep}"
+            # eager work between replays
+            ext.moe_layer(layer, dense, x, shape.top_k, workspace=ws)
+        del graph
+    finally:
+        ext.set_option(_native.UQM_OPT_OVERLAP_SHARED, 1)
+
+
 def test_c4_prefill_512_tokens(mfma_on):
     """c4: 512 tokens through the whole block (MFMA routed + shared). Every
     token's result depends only on its own routes, so 16 sampled tokens are

@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 #include <string>
 
 #include "../../include/uma_qmoe_hip.h"
@@ -87,6 +88,7 @@ P* at(void* ws, size_t off) {
 std::atomic<int64_t> g_opt_fused{1};
 std::atomic<int64_t> g_opt_fused_routed_blocks{0};
 std::atomic<int64_t> g_opt_mfma_min_tokens{2};
+std::atomic<int64_t> g_opt_overlap_shared{1};
 
 // Compute units of the current device (cached per device id).
 std::atomic<int> g_cus[64];
@@ -162,6 +164,46 @@ int routed_tile_tokens(const uqm_expert_weights* w, int64_t T, int64_t k) {
   const int64_t active = R < w->num_experts ? R : w->num_experts;
   const double mean = static_cast<double>(R) / static_cast<double>(active);
   return 16 * (mean >= 16 ? 2 : nb_for(w->encoding, mean));
+}
+
+// Per-device side stream and fork/join events: a multi-token block runs the
+// shared expert (which reads only the input) on the side stream, beside the
+// router -> top-k -> permute -> routed chain on the caller's stream, and the
+// combine waits for both. The mutex is held from the fork to the join so that
+// two host threads never interleave records of the same events. The stream is
+// non-blocking (no implicit sync with the legacy default stream) and keeps the
+// default priority.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_side_mu;
+SideStream g_side[64];
+
+// Side stream of the current device, created on first use; nullptr when it
+// does not exist yet and `caller` is being captured into a graph (creation
+// is not a capturable call), or when creation fails: the caller then runs the
+// shared expert in order on its own stream.
+SideStream* side_stream(hipStream_t caller) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  SideStream& ss = g_side[dev];
+  if (ss.stream != nullptr) return &ss;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(caller, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
+  hipStream_t s = nullptr;
+  hipEvent_t f = nullptr, j = nullptr;
+  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+  if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+    if (f != nullptr) (void)hipEventDestroy(f);
+    (void)hipStreamDestroy(s);
+    return nullptr;
+  }
+  ss.fork = f;
+  ss.join = j;
+  ss.stream = s;
+  return &ss;
 }
 
 // Per-device verdict of the gfx950 check: 0 unknown, 1 gfx950, 2 other.
@@ -685,6 +727,23 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
       return rc;
     x = xn;
   }
+  // 4 (forked). shared expert on the side stream, beside steps 1-3
+  int ys_parts = 1;
+  std::unique_lock<std::mutex> side_lock;
+  SideStream* side = nullptr;
+  if (layer->has_shared) {
+    if (g_opt_overlap_shared.load(std::memory_order_relaxed) != 0) {
+      side_lock = std::unique_lock<std::mutex>(g_side_mu);
+      side = side_stream(s);
+    }
+    if (side != nullptr) {
+      if ((rc = hip_check(hipEventRecord(side->fork, s), "fork record")) ||
+          (rc = hip_check(hipStreamWaitEvent(side->stream, side->fork, 0), "fork wait")))
+        return rc;
+      if ((rc = run_shared(layer, x, tokens, H, L, workspace, &ys_parts, side->stream))) return rc;
+      if ((rc = hip_check(hipEventRecord(side->join, side->stream), "join record"))) return rc;
+    }
+  }
   // 1-2. router logits (+ shared-gate logit in column E), top-k
   uint16_t* wout = routing_weights != nullptr ? static_cast<uint16_t*>(routing_weights) : at<uint16_t>(workspace, L.weights);
   int64_t* iout = expert_indices != nullptr ? expert_indices : at<int64_t>(workspace, L.indices);
@@ -731,10 +790,14 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
                       "permute launch")))
     return rc;
   // 3. routed experts
-  int yr_parts = 1, ys_parts = 1;
+  int yr_parts = 1;
   if ((rc = run_routed(w, x, tokens, k, L, workspace, tile_tokens, &yr_parts, s))) return rc;
-  // 4. shared expert
-  if (layer->has_shared && (rc = run_shared(layer, x, tokens, H, L, workspace, &ys_parts, s))) return rc;
+  // 4. shared expert (joined, or in order on the caller's stream)
+  if (side != nullptr) {
+    if ((rc = hip_check(hipStreamWaitEvent(s, side->join, 0), "join wait"))) return rc;
+  } else if (layer->has_shared && (rc = run_shared(layer, x, tokens, H, L, workspace, &ys_parts, s))) {
+    return rc;
+  }
   // 5. combine
   return hip_check(launch_combine(at<float>(workspace, L.y_routed), yr_parts, tokens * k * H, wout, iout, tokens, k, E,
                                   H, layer->has_shared ? at<float>(workspace, L.y_shared) : nullptr, ys_parts,
@@ -770,6 +833,9 @@ int uqm_set_option(int option, int64_t value) {
     case UQM_OPT_MFMA_MIN_TOKENS:
       if (value < 0) return fail(UQM_ERR_ARGUMENT, "token threshold must be >= 0");
       g_opt_mfma_min_tokens.store(value);
+      return UQM_OK;
+    case UQM_OPT_OVERLAP_SHARED:
+      g_opt_overlap_shared.store(value != 0 ? 1 : 0);
       return UQM_OK;
     default:
       return fail(UQM_ERR_ARGUMENT, "unknown option %d", option);

@@ -38,14 +38,25 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
   const uint16_t* row = plog != nullptr ? nullptr : logits + t * ldl;
   const float* prow = plog != nullptr ? plog + t * ldl : nullptr;
 
+  // column E (the shared-expert gate logit) is loaded with the others, by
+  // lane E % 64 (lane 0 when E = 256), so that the block has a single round
+  // trip of loads
   float l[4];
+  float gate = 0.f;
+  if (shared_gate != nullptr && E >= 256 && lane == 0) gate = logit_of(row, prow, parts, pstride, E);
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
-    l[i] = e < E ? logit_of(row, prow, parts, pstride, e) : -INFINITY;
-    if (logits_out != nullptr && e < E) logits_out[t * E + e] = f32_to_bf16(l[i]);
-    mx = fmaxf(mx, l[i]);
+    const bool load = e < E || (shared_gate != nullptr && e == E);
+    float v = load ? logit_of(row, prow, parts, pstride, e) : -INFINITY;
+    if (e == E) {
+      gate = v;
+      v = -INFINITY;
+    }
+    l[i] = v;
+    if (logits_out != nullptr && e < E) logits_out[t * E + e] = f32_to_bf16(v);
+    mx = fmaxf(mx, v);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
@@ -91,8 +102,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
     indices_out[t * k + lane] = my_e;
     if (route_expert != nullptr) route_expert[t * k + lane] = my_e;
   }
-  if (shared_gate != nullptr && lane == 0)
-    shared_gate[t] = round_bf16(sigmoidf_(logit_of(row, prow, parts, pstride, E)));
+  if (shared_gate != nullptr && lane == (E < 256 ? (E & 63) : 0)) shared_gate[t] = round_bf16(sigmoidf_(gate));
 }
 
 hipError_t launch_route_topk(const uint16_t* logits, int64_t ldl, int64_t T, int64_t E, int64_t k, int norm,

@@ -22,6 +22,7 @@ UQM_BF16 = 2
 UQM_OPT_FUSED_DECODE = 1
 UQM_OPT_FUSED_ROUTED_BLOCKS = 2
 UQM_OPT_MFMA_MIN_TOKENS = 3
+UQM_OPT_OVERLAP_SHARED = 4
 
 ENCODING_IDS = {"q4_group128": UQM_Q4, "q8_group128": UQM_Q8, "bf16_le": UQM_BF16}
 
