@@ -22,10 +22,12 @@
  *     the side stream and its two events are created once per device);
  *     temporaries live in the caller's `workspace`, sized by
  *     uqm_moe_workspace_bytes(). The workspace must be zero-filled before its
- *     first use: its first 4352 bytes hold the single-token fused kernel's
- *     synchronisation words (an error word and one launch epoch per
- *     workgroup, advanced by every launch). Calls in order on one stream may
- *     reuse a workspace; calls that overlap in time must not share one.
+ *     first use: its first 4352 bytes hold synchronisation words (the
+ *     single-token fused kernel's error word and one launch epoch per
+ *     workgroup, advanced by every launch, and a completion counter that
+ *     multi-token calls leave at zero). Calls in order on one stream may
+ *     reuse a workspace, also with different token counts; calls that
+ *     overlap in time must not share one.
  *   - Return 0 on success, nonzero UQM_ERR_* otherwise; the message is in
  *     uqm_last_error() (thread-local). Invalid arguments are rejected before
  *     any launch.

@@ -290,6 +290,36 @@ def test_moe_layer_matches_oracle_block(hip_ext, name, t):
     assert_close(out, ref, f"{shape.name} block t={t}")
 
 
+@pytest.mark.parametrize("t", [768, 769])
+def test_block_topk_permute_fusion_boundary(hip_ext, t):
+    """768 tokens x top-4 = 3072 routes take the top-k and the permutation in
+    one launch (the last workgroup to finish its top-k permutes), 769 tokens
+    take two launches. Indices follow the kernel's logits exactly, sampled
+    tokens match the oracle block, and a second call on the same workspace
+    (whose completion counter the first call must leave at zero) gives the
+    same bits."""
+    shape = syn.MoEShape("routes_3072", 256, 16, 4, 128, 128)
+    note(f"top-k + permute fusion boundary t={t}")
+    layer = syn.build_experts(shape, device=DEV)
+    dense = syn.build_dense(shape, device=DEV)
+    reader = syn.DeviceLayerReader({0: layer})
+    x = syn.hidden_states(shape, t, seed=5)
+    out, logits, weights, indices = hip_ext.moe_layer(layer, dense, x.to(DEV), shape.top_k)
+    out = out.clone()
+    logits_c, weights_c, indices_c = logits.cpu(), weights.cpu(), indices.cpu()
+    assert torch.equal(indices_c, om.topk_ordered(logits_c, shape.top_k))
+    dense_c = DenseBlock(*(None if v is None else v.cpu() for v in (
+        dense.router, dense.shared_gate, dense.shared_up, dense.shared_down, dense.shared_expert_gate)))
+    lay = {"router": dense_c.router, "top_k": shape.top_k, "num_experts": shape.num_experts,
+           "shared_gate": dense_c.shared_gate, "shared_up": dense_c.shared_up, "shared_down": dense_c.shared_down,
+           "shared_expert_gate": dense_c.shared_expert_gate}
+    pick = torch.randperm(t, generator=torch.Generator().manual_seed(t))[:16].sort().values
+    ref, *_ = om.qwen_block(x[pick], lay, reader, 0, routes=(weights_c[pick], indices_c[pick]))
+    assert_close(out.cpu()[pick], ref, f"sampled tokens t={t}")
+    again = hip_ext.moe_layer(layer, dense, x.to(DEV), shape.top_k)[0]
+    assert torch.equal(again, out)
+
+
 @pytest.mark.parametrize("layer_index", [0, 16])
 def test_c3_stack_layer_encodings(hip_ext, layer_index):
     """c3: routed BF16 (layers 0-15) and Q8 (layers 16-23) blocks with shared expert."""

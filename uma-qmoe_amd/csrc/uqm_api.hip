@@ -268,7 +268,8 @@ bool router_uses_mfma(int64_t H, int64_t T) {
 // bf16 linear. logits (optional) receives the bf16 logits [T, E].
 int run_router_mfma(const void* router, const void* gate_row, int64_t E, const uint16_t* x, int64_t T, int64_t H,
                     int64_t k, int norm, const Layout& L, void* ws, uint16_t* wout, int64_t* iout,
-                    int32_t* route_expert, float* sg, uint16_t* logits, hipStream_t stream) {
+                    int32_t* route_expert, float* sg, uint16_t* logits, const uqm::RouteTables* perm,
+                    int tile_tokens, uint32_t* counter, hipStream_t stream) {
   using namespace uqm;
   const int64_t rows = E + (gate_row != nullptr ? 1 : 0);
   const int64_t rp = (rows + 15) / 16 * 16;
@@ -297,6 +298,10 @@ int run_router_mfma(const void* router, const void* gate_row, int64_t E, const u
   r.ksplit = ks < 1 ? 1 : static_cast<int>(ks);
   int rc = hip_check(launch_expert_mfma(UQM_BF16, 1, r, 1, 4, 4, cus, stream), "router MFMA launch");
   if (rc) return rc;
+  if (perm != nullptr)
+    return hip_check(launch_route_topk_permute(nullptr, at<float>(ws, L.router_part), r.ksplit, T * rp, rp, T, E, k,
+                                               norm, wout, iout, sg, logits, *perm, tile_tokens, counter, stream),
+                     "top-k + permute launch");
   return hip_check(launch_route_topk_partials(at<float>(ws, L.router_part), r.ksplit, T * rp, rp, T, E, k, norm, wout,
                                               iout, route_expert, sg, logits, stream),
                    "top-k launch");
@@ -573,7 +578,7 @@ int uqm_router_topk(const void* hidden, int64_t tokens, int64_t hidden_size, con
   if (router_uses_mfma(hidden_size, tokens))
     return run_router_mfma(router, nullptr, num_experts, static_cast<const uint16_t*>(hidden), tokens, hidden_size,
                            top_k, norm_topk_prob, L, workspace, static_cast<uint16_t*>(routing_weights),
-                           expert_indices, nullptr, nullptr, static_cast<uint16_t*>(logits), s);
+                           expert_indices, nullptr, nullptr, static_cast<uint16_t*>(logits), nullptr, 0, nullptr, s);
   uint16_t* lg = logits != nullptr ? static_cast<uint16_t*>(logits) : at<uint16_t>(workspace, L.logits);
   GemvArgs a{};
   a.w[0] = static_cast<const uint8_t*>(router);
@@ -752,10 +757,15 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
                  at<int32_t>(workspace, L.expert_offsets), at<int32_t>(workspace, L.active_experts),
                  at<int32_t>(workspace, L.counters), at<int32_t>(workspace, L.tiles),
                  at<int32_t>(workspace, L.counters) + 1};
+  // top-k and the permutation in one launch when the routes fit one workgroup
+  const int tile_tokens = routed_tile_tokens(w, tokens, k);
+  const bool fuse_permute = route_topk_permute_fits(tokens, k);
+  uint32_t* permute_counter = at<uint32_t>(workspace, L.fused_sync) + kSyncPermuteDone;
   if (router_uses_mfma(H, tokens)) {
     if ((rc = run_router_mfma(layer->router, layer->has_shared ? layer->shared_expert_gate : nullptr, E, x, tokens, H,
                               k, layer->norm_topk_prob, L, workspace, wout, iout, rt.route_expert, sg,
-                              static_cast<uint16_t*>(logits), s)))
+                              static_cast<uint16_t*>(logits), fuse_permute ? &rt : nullptr, tile_tokens,
+                              permute_counter, s)))
       return rc;
   } else {
     uint16_t* lg = at<uint16_t>(workspace, L.logits);
@@ -774,10 +784,17 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
     r.out = lg;
     r.ldo = rows_router;
     if ((rc = hip_check(launch_expert_gemv(UQM_BF16, 1, kModeBF16, r, 1, nt, s), "router launch"))) return rc;
-    if ((rc = hip_check(launch_route_topk(lg, rows_router, tokens, E, k, layer->norm_topk_prob, wout, iout,
-                                          rt.route_expert, sg, s),
-                        "top-k launch")))
+    if (fuse_permute) {
+      if ((rc = hip_check(launch_route_topk_permute(lg, nullptr, 1, 0, rows_router, tokens, E, k,
+                                                    layer->norm_topk_prob, wout, iout, sg, nullptr, rt, tile_tokens,
+                                                    permute_counter, s),
+                          "top-k + permute launch")))
+        return rc;
+    } else if ((rc = hip_check(launch_route_topk(lg, rows_router, tokens, E, k, layer->norm_topk_prob, wout, iout,
+                                                 rt.route_expert, sg, s),
+                               "top-k launch"))) {
       return rc;
+    }
     if (logits != nullptr) {
       if ((rc = hip_check(hipMemcpy2DAsync(logits, 2 * E, lg, 2 * rows_router, 2 * E, tokens, hipMemcpyDeviceToDevice,
                                            s),
@@ -785,8 +802,8 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
         return rc;
     }
   }
-  const int tile_tokens = routed_tile_tokens(w, tokens, k);
-  if ((rc = hip_check(launch_route_permute(rt.route_expert, nullptr, tokens * k, E, rt, nullptr, nullptr, tile_tokens, s),
+  if (!fuse_permute &&
+      (rc = hip_check(launch_route_permute(rt.route_expert, nullptr, tokens * k, E, rt, nullptr, nullptr, tile_tokens, s),
                       "permute launch")))
     return rc;
   // 3. routed experts

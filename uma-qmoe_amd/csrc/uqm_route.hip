@@ -23,18 +23,12 @@ __device__ __forceinline__ float logit_of(const uint16_t* row, const float* prow
   return round_bf16(v);
 }
 
-__global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restrict__ logits,
-                                                         const float* __restrict__ plog, int parts, int64_t pstride,
-                                                         int64_t ldl, int64_t T, int E, int k, int norm,
-                                                         uint16_t* __restrict__ weights_out,
-                                                         int64_t* __restrict__ indices_out,
-                                                         int32_t* __restrict__ route_expert,
-                                                         float* __restrict__ shared_gate,
-                                                         uint16_t* __restrict__ logits_out) {
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + wave;
-  if (t >= T) return;
+// Top-k, softmax weights and shared-expert gate of token t, by one wavefront.
+__device__ __forceinline__ void topk_token(int64_t t, int lane, const uint16_t* __restrict__ logits,
+                                           const float* __restrict__ plog, int parts, int64_t pstride, int64_t ldl,
+                                           int E, int k, int norm, uint16_t* __restrict__ weights_out,
+                                           int64_t* __restrict__ indices_out, int32_t* __restrict__ route_expert,
+                                           float* __restrict__ shared_gate, uint16_t* __restrict__ logits_out) {
   const uint16_t* row = plog != nullptr ? nullptr : logits + t * ldl;
   const float* prow = plog != nullptr ? plog + t * ldl : nullptr;
 
@@ -100,9 +94,28 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restr
   if (lane < k) {
     weights_out[t * k + lane] = f32_to_bf16(p);
     indices_out[t * k + lane] = my_e;
-    if (route_expert != nullptr) route_expert[t * k + lane] = my_e;
+    // device-coherent store: the fused top-k + permutation launch reads the
+    // ids back in another workgroup, possibly on another XCD
+    if (route_expert != nullptr)
+      __hip_atomic_store(route_expert + t * k + lane, my_e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (shared_gate != nullptr && lane == (E < 256 ? (E & 63) : 0)) shared_gate[t] = round_bf16(sigmoidf_(gate));
+}
+
+__global__ __launch_bounds__(256) void route_topk_kernel(const uint16_t* __restrict__ logits,
+                                                         const float* __restrict__ plog, int parts, int64_t pstride,
+                                                         int64_t ldl, int64_t T, int E, int k, int norm,
+                                                         uint16_t* __restrict__ weights_out,
+                                                         int64_t* __restrict__ indices_out,
+                                                         int32_t* __restrict__ route_expert,
+                                                         float* __restrict__ shared_gate,
+                                                         uint16_t* __restrict__ logits_out) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (t >= T) return;
+  topk_token(t, lane, logits, plog, parts, pstride, ldl, E, k, norm, weights_out, indices_out, route_expert,
+             shared_gate, logits_out);
 }
 
 hipError_t launch_route_topk(const uint16_t* logits, int64_t ldl, int64_t T, int64_t E, int64_t k, int norm,
@@ -128,10 +141,20 @@ hipError_t launch_route_topk_partials(const float* plog, int parts, int64_t pstr
   return hipGetLastError();
 }
 
+// kCoherent: read route_expert with device-coherent loads (ids written by
+// other workgroups of the same launch).
+template <bool kCoherent = false>
 __device__ __forceinline__ int load_route_id(const int32_t* route_expert, const int64_t* indices64, int64_t r,
                                              int64_t n, int E, bool& valid) {
   int64_t id = -1;
-  if (r < n) id = indices64 != nullptr ? indices64[r] : static_cast<int64_t>(route_expert[r]);
+  if (r < n) {
+    if (indices64 != nullptr)
+      id = indices64[r];
+    else if constexpr (kCoherent)
+      id = __hip_atomic_load(const_cast<int32_t*>(route_expert) + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      id = route_expert[r];
+  }
   valid = id >= 0 && id < E;
   return valid ? static_cast<int>(id) : 0;
 }
@@ -281,14 +304,21 @@ __global__ __launch_bounds__(64) void route_permute_kernel(const int32_t* __rest
 constexpr int kPermuteMaxRoutes = 3072;
 constexpr int kPermuteWaves = 16;
 
-__global__ __launch_bounds__(64 * kPermuteWaves) void route_permute_wg_kernel(
-    const int32_t* __restrict__ route_expert, const int64_t* __restrict__ indices64, int64_t n, int E,
-    int32_t* __restrict__ route_order, int32_t* __restrict__ expert_offsets, int32_t* __restrict__ active_experts,
-    int32_t* __restrict__ active_count, int64_t* __restrict__ order64, int64_t* __restrict__ offsets64,
-    int tile_tokens, int32_t* __restrict__ tiles, int32_t* __restrict__ tile_count) {
+// Body of the one-workgroup permutation (kPermuteWaves wavefronts).
+template <bool kCoherent>
+__device__ __forceinline__ void permute_wg(const int32_t* __restrict__ route_expert,
+                                           const int64_t* __restrict__ indices64, int64_t n, int E,
+                                           int32_t* __restrict__ route_order, int32_t* __restrict__ expert_offsets,
+                                           int32_t* __restrict__ active_experts, int32_t* __restrict__ active_count,
+                                           int64_t* __restrict__ order64, int64_t* __restrict__ offsets64,
+                                           int tile_tokens, int32_t* __restrict__ tiles,
+                                           int32_t* __restrict__ tile_count) {
   constexpr int kChunks = kPermuteMaxRoutes / 64;
   constexpr int kPer = kChunks / kPermuteWaves;  // chunks per wavefront
-  __shared__ int hist[kChunks][256];
+  // [chunk][expert] counts in dynamic LDS sized for the launch's chunks
+  // (permute_lds_bytes), so a small permutation fits beside other kernels
+  extern __shared__ int hist_dyn[];
+  int (*hist)[256] = reinterpret_cast<int (*)[256]>(hist_dyn);
   __shared__ int cnt[256];
   __shared__ int start[256];
   const int wave = threadIdx.x >> 6;
@@ -310,7 +340,7 @@ __global__ __launch_bounds__(64 * kPermuteWaves) void route_permute_wg_kernel(
     ranks[j] = 0;
     if (ch < nch) {  // uniform over the wavefront
       bool valid;
-      const int id = load_route_id(route_expert, indices64, static_cast<int64_t>(ch) * 64 + lane, n, E, valid);
+      const int id = load_route_id<kCoherent>(route_expert, indices64, static_cast<int64_t>(ch) * 64 + lane, n, E, valid);
       const uint64_t eq = same_id_lanes(id, valid, nbits);
       ids[j] = id;
       oks[j] = valid;
@@ -346,12 +376,73 @@ __global__ __launch_bounds__(64 * kPermuteWaves) void route_permute_wg_kernel(
   }
 }
 
+// Dynamic LDS of permute_wg for n routes.
+size_t permute_lds_bytes(int64_t n) { return static_cast<size_t>((n + 63) / 64) * 256 * sizeof(int); }
+
+__global__ __launch_bounds__(64 * kPermuteWaves) void route_permute_wg_kernel(
+    const int32_t* __restrict__ route_expert, const int64_t* __restrict__ indices64, int64_t n, int E,
+    int32_t* __restrict__ route_order, int32_t* __restrict__ expert_offsets, int32_t* __restrict__ active_experts,
+    int32_t* __restrict__ active_count, int64_t* __restrict__ order64, int64_t* __restrict__ offsets64,
+    int tile_tokens, int32_t* __restrict__ tiles, int32_t* __restrict__ tile_count) {
+  permute_wg<false>(route_expert, indices64, n, E, route_order, expert_offsets, active_experts, active_count, order64,
+             offsets64, tile_tokens, tiles, tile_count);
+}
+
+// Top-k and permutation in one launch (up to kPermuteMaxRoutes routes): one
+// token per wavefront. The route ids are written with device-coherent stores;
+// once they have completed, every workgroup counts itself done on a
+// device-scope counter, and the workgroup that arrives last reads the ids back
+// with device-coherent loads, runs the permutation and resets the counter for
+// the next launch. Nothing waits on another workgroup, and no cache is
+// written back or invalidated.
+__global__ __launch_bounds__(64 * kPermuteWaves) void route_topk_permute_kernel(
+    const uint16_t* __restrict__ logits, const float* __restrict__ plog, int parts, int64_t pstride, int64_t ldl,
+    int64_t T, int E, int k, int norm, uint16_t* __restrict__ weights_out, int64_t* __restrict__ indices_out,
+    float* __restrict__ shared_gate, uint16_t* __restrict__ logits_out, RouteTables rt, int tile_tokens,
+    uint32_t* __restrict__ counter) {
+  __shared__ int s_last;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kPermuteWaves + wave;
+  if (t < T)
+    topk_token(t, lane, logits, plog, parts, pstride, ldl, E, k, norm, weights_out, indices_out, rt.route_expert,
+               shared_gate, logits_out);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t done = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = done == gridDim.x - 1 ? 1 : 0;
+  }
+  __syncthreads();
+  if (s_last == 0) return;
+  permute_wg<true>(rt.route_expert, nullptr, T * k, E, rt.route_order, rt.expert_offsets, rt.active_experts,
+             rt.active_count, nullptr, nullptr, tile_tokens, rt.tiles, rt.tile_count);
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+bool route_topk_permute_fits(int64_t T, int64_t k) { return T > 0 && T * k <= kPermuteMaxRoutes; }
+
+hipError_t launch_route_topk_permute(const uint16_t* logits, const float* plog, int parts, int64_t pstride,
+                                     int64_t ldl, int64_t T, int64_t E, int64_t k, int norm, uint16_t* weights_out,
+                                     int64_t* indices_out, float* shared_gate, uint16_t* logits_out,
+                                     const RouteTables& rt, int tile_tokens, uint32_t* counter, hipStream_t stream) {
+  if (!route_topk_permute_fits(T, k) || counter == nullptr) return hipErrorInvalidValue;
+  if (tile_tokens > 0 && (rt.tiles == nullptr || rt.tile_count == nullptr)) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>((T + kPermuteWaves - 1) / kPermuteWaves));
+  hipLaunchKernelGGL(route_topk_permute_kernel, grid, dim3(64 * kPermuteWaves), permute_lds_bytes(T * k), stream,
+                     logits, plog,
+                     plog != nullptr ? parts : 1, pstride, ldl, T, static_cast<int>(E), static_cast<int>(k), norm,
+                     weights_out, indices_out, shared_gate, logits_out, rt, tile_tokens, counter);
+  return hipGetLastError();
+}
+
 hipError_t launch_route_permute(const int32_t* route_expert, const int64_t* indices64, int64_t n_routes,
                                 int64_t E, const RouteTables& rt, int64_t* order64, int64_t* offsets64,
                                 int tile_tokens, hipStream_t stream) {
   if (tile_tokens > 0 && (rt.tiles == nullptr || rt.tile_count == nullptr)) return hipErrorInvalidValue;
   if (n_routes > 64 && n_routes <= kPermuteMaxRoutes)
-    hipLaunchKernelGGL(route_permute_wg_kernel, dim3(1), dim3(64 * kPermuteWaves), 0, stream, route_expert, indices64,
+    hipLaunchKernelGGL(route_permute_wg_kernel, dim3(1), dim3(64 * kPermuteWaves), permute_lds_bytes(n_routes), stream,
+                       route_expert, indices64,
                        n_routes, static_cast<int>(E), rt.route_order, rt.expert_offsets, rt.active_experts,
                        rt.active_count, order64, offsets64, tile_tokens, rt.tiles, rt.tile_count);
   else
