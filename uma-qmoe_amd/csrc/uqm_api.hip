@@ -11,6 +11,7 @@
 
 #include "../../include/uma_qmoe_hip.h"
 #include "uqm_internal.h"
+#include "uqm_route.h"
 
 namespace {
 

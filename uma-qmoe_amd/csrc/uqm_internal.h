@@ -116,27 +116,16 @@ hipError_t launch_route_permute(const int32_t* route_expert, const int64_t* indi
                                 int64_t E, const RouteTables& rt, int64_t* order64, int64_t* offsets64,
                                 int tile_tokens, hipStream_t stream);
 
-// Top-k (over bf16 logits, or over `parts` FP32 partials when plog is set)
-// and the permutation of its routes into rt, in one launch. `counter` is a
-// workspace word that is zero before the launch and zero again after it.
-bool route_topk_permute_fits(int64_t T, int64_t k);
-hipError_t launch_route_topk_permute(const uint16_t* logits, const float* plog, int parts, int64_t pstride,
-                                     int64_t ldl, int64_t T, int64_t E, int64_t k, int norm, uint16_t* weights_out,
-                                     int64_t* indices_out, float* shared_gate, uint16_t* logits_out,
-                                     const RouteTables& rt, int tile_tokens, uint32_t* counter, hipStream_t stream);
-
 // out[t, o] = bf16( sum_s w[t,s] * y[t*k+s, o] + sg[t] * ys[t, o] ), where y and
 // ys are the sums of y_parts / ys_parts FP32 partials spaced by *_stride elements.
 hipError_t launch_combine(const float* y, int y_parts, int64_t y_stride, const uint16_t* weights,
                           const int64_t* indices, int64_t T, int64_t k, int64_t E, int64_t H, const float* ys,
                           int ys_parts, int64_t ys_stride, const float* sg, uint16_t* out, hipStream_t stream);
-// Sync words at the start of every workspace, at offsets that do not depend on
-// the token count (zero before the first launch): a sticky error word the
-// single-token fused kernel (uqm_fused.hip) raises when one of its bounded
-// waits expires, the completion counter of the fused top-k + permutation
-// launch (back to zero after every launch), and one launch epoch per
-// workgroup of the fused kernel that the workgroup advances on every launch.
-enum : int { kSyncError = 4, kSyncPermuteDone = 8, kSyncEpochBase = 64 };
+// Single-token fused MoE block (uqm_fused.hip). Sync words live in `sync`
+// (zero before the first launch): a sticky error word the kernel raises when
+// one of its bounded waits expires, and one launch epoch per workgroup that
+// the workgroup advances on every launch.
+enum : int { kSyncError = 4, kSyncEpochBase = 64 };
 constexpr int kMaxFusedBlocks = 1024;  // workgroups (one per CU)
 constexpr int kSyncWords = kSyncEpochBase + kMaxFusedBlocks;
 

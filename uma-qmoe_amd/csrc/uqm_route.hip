@@ -10,7 +10,7 @@
 // 64-route chunk, eight wave ballots give every lane the mask of lanes holding
 // the same expert id, so ranks come from one popcount and no comparison sort
 // is needed (one workgroup up to 3072 routes, one wavefront beyond).
-#include "uqm_internal.h"
+#include "uqm_route.h"
 
 namespace uqm {
 
