@@ -740,6 +740,18 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
   int ys_parts = 1;
   std::unique_lock<std::mutex> side_lock;
   SideStream* side = nullptr;
+  // Once forked, the side stream is joined back into the caller's stream on
+  // every return path (an error return included), so that a graph capture of
+  // the caller's stream never ends with an unjoined branch.
+  struct JoinOnExit {
+    hipStream_t caller;
+    SideStream* side = nullptr;
+    ~JoinOnExit() {
+      if (side == nullptr) return;
+      (void)hipEventRecord(side->join, side->stream);
+      (void)hipStreamWaitEvent(caller, side->join, 0);
+    }
+  } join_on_exit{s};
   if (layer->has_shared) {
     if (g_opt_overlap_shared.load(std::memory_order_relaxed) != 0) {
       side_lock = std::unique_lock<std::mutex>(g_side_mu);
@@ -749,8 +761,8 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
       if ((rc = hip_check(hipEventRecord(side->fork, s), "fork record")) ||
           (rc = hip_check(hipStreamWaitEvent(side->stream, side->fork, 0), "fork wait")))
         return rc;
+      join_on_exit.side = side;
       if ((rc = run_shared(layer, x, tokens, H, L, workspace, &ys_parts, true, side->stream))) return rc;
-      if ((rc = hip_check(hipEventRecord(side->join, side->stream), "join record"))) return rc;
     }
   }
   // 1-2. router logits (+ shared-gate logit in column E), top-k
@@ -815,7 +827,10 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
   if ((rc = run_routed(w, x, tokens, k, L, workspace, tile_tokens, &yr_parts, s))) return rc;
   // 4. shared expert (joined, or in order on the caller's stream)
   if (side != nullptr) {
-    if ((rc = hip_check(hipStreamWaitEvent(s, side->join, 0), "join wait"))) return rc;
+    join_on_exit.side = nullptr;
+    if ((rc = hip_check(hipEventRecord(side->join, side->stream), "join record")) ||
+        (rc = hip_check(hipStreamWaitEvent(s, side->join, 0), "join wait")))
+      return rc;
   } else if (layer->has_shared && (rc = run_shared(layer, x, tokens, H, L, workspace, &ys_parts, false, s))) {
     return rc;
   }
