@@ -56,7 +56,8 @@ enum { UQM_Q4 = 0, UQM_Q8 = 1, UQM_BF16 = 2 };
 
 /* Options for uqm_set_option (process-wide). */
 enum {
-  UQM_OPT_FUSED_DECODE = 1,   /* 1 (default): single-token blocks use the fused persistent kernel */
+  UQM_OPT_FUSED_DECODE = 1,   /* 1 (default): blocks of one or two tokens use the fused persistent
+                                  kernel, one launch per token */
   UQM_OPT_FUSED_ROUTED_BLOCKS = 2, /* accepted, no effect: every CU of the fused kernel takes a share
                                       of every phase (values 0..4096 as before) */
   UQM_OPT_MFMA_MIN_TOKENS = 3,     /* token count from which multi-token calls run the expert projections
@@ -164,9 +165,9 @@ int uqm_moe_forward(const uqm_expert_weights* weights, const void* hidden, int64
  * (src/uma_qmoe/qwen_compressed_loader.py:67-86) and QuantizedMoEBlock.forward
  * (src/uma_qmoe/compressed_loader.py:58-67). logits [tokens, E] bf16,
  * routing_weights [tokens, k] bf16 and expert_indices [tokens, k] int64 are
- * optional outputs (NULL to skip). With tokens == 1 and a supported shape
+ * optional outputs (NULL to skip). With tokens <= 2 and a supported shape
  * (H = 2048, I/Is giving 1-3 / 11 chunks per lane, top_k <= 8, Q4/Q8/BF16)
- * the whole block is one persistent launch (see uqm_set_option). */
+ * the whole block is one persistent launch per token (see uqm_set_option). */
 int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, void* output, void* logits,
                   void* routing_weights, int64_t* expert_indices, void* workspace, size_t workspace_bytes,
                   void* stream);

@@ -131,13 +131,13 @@ def _norm_case(case):
 
 # (tokens, fused option): one token on the fused kernel and on the multi-kernel
 # path; three tokens take the multi-kernel path whatever the option
-@pytest.mark.parametrize("tokens,fused", [(1, 1), (1, 0), (3, 1)])
+@pytest.mark.parametrize("tokens,fused", [(1, 1), (1, 0), (2, 1), (3, 1)])
 @pytest.mark.parametrize("weighted", [False, True])
 @pytest.mark.parametrize("case", ["c1", "c2", "c3_l0", "c3_l16"])
 def test_norm_block_matches_oracle(fused_default, case, weighted, tokens, fused):
     """MoE(RMSNorm(x)) in one call (folded into the fused kernel's activation
-    staging for one token) against the oracle's RMSNorm followed by its block,
-    given the device's routes."""
+    staging: one launch per token up to two tokens) against the oracle's
+    RMSNorm followed by its block, given the device's routes."""
     hip_ext = fused_default
     note(f"norm block {case} weighted={weighted} tokens={tokens} fused={fused}")
     hip_ext.set_option(_native.UQM_OPT_FUSED_DECODE, fused)

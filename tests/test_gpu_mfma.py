@@ -78,9 +78,12 @@ def routes(t, k, e, seed, hot=None, hot_share=0.0):
 
 @pytest.fixture
 def mfma_on(hip_ext):
+    # two-token blocks would take the fused kernel once per token
     hip_ext.set_option(_native.UQM_OPT_MFMA_MIN_TOKENS, 2)
+    hip_ext.set_option(_native.UQM_OPT_FUSED_DECODE, 0)
     yield hip_ext
     hip_ext.set_option(_native.UQM_OPT_MFMA_MIN_TOKENS, 2)
+    hip_ext.set_option(_native.UQM_OPT_FUSED_DECODE, 1)
 
 
 def both_paths(ext, fn):
