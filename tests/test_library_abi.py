@@ -44,3 +44,28 @@ def test_struct_layouts_match_header():
     # uqm_expert_weights: 2 x int32, 3 x int64, 6 pointers
     assert ctypes.sizeof(_native.ExpertWeights) == 8 + 3 * 8 + 6 * 8
     assert ctypes.sizeof(_native.LayerWeights) == ctypes.sizeof(_native.ExpertWeights) + 8 + 8 + 4 + 4 + 8 + 4 * 8
+
+
+def header_enum_values() -> dict[str, int]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    values = {}
+    for body in re.findall(r"enum\s*\{(.*?)\}", text, flags=re.S):
+        for name, value in re.findall(r"\b(UQM_[A-Z0-9_]+)\s*=\s*(\d+)", body):
+            values[name] = int(value)
+    return values
+
+
+def test_python_constants_match_header_enums():
+    values = header_enum_values()
+    for name in ("UQM_Q4", "UQM_Q8", "UQM_BF16", "UQM_OPT_FUSED_DECODE", "UQM_OPT_FUSED_ROUTED_BLOCKS",
+                 "UQM_OPT_MFMA_MIN_TOKENS", "UQM_OPT_OVERLAP_SHARED"):
+        assert values[name] == getattr(_native, name), name
+
+
+def test_set_option_is_host_only_and_validates():
+    lib = _native.library()
+    assert lib.uqm_set_option(_native.UQM_OPT_OVERLAP_SHARED, 0) == 0
+    assert lib.uqm_set_option(_native.UQM_OPT_OVERLAP_SHARED, 1) == 0
+    assert lib.uqm_set_option(99, 1) != 0
+    assert b"unknown option" in lib.uqm_last_error()
+    assert lib.uqm_set_option(_native.UQM_OPT_MFMA_MIN_TOKENS, -1) != 0
