@@ -47,6 +47,9 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch32", dest="batch32", action="store_false",
                     help="skip the batch-32 decode measurement reported beside the batch-1 value")
+    ap.add_argument("--multi-kernel", action="store_true",
+                    help="one- and two-token calls take the multi-launch path (UQM_OPT_FUSED_DECODE = 0) "
+                         "instead of the fused kernel")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 8 device-to-device copies of BYTES bytes (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against a kernel of known traffic) and exit")
@@ -422,12 +425,15 @@ def main() -> int:
         print(json.dumps({"copy_probe_bytes": args.copy_probe, "copies": 8}), flush=True)
         return 0
 
+    from uma_qmoe_amd import _native
     from uma_qmoe_amd import synthetic as syn
     from uma_qmoe_amd.native_backend import load_native_extension
 
     _platform, ext = load_native_extension()
     if args.config == "c3":
         return main_stack(args, torch, syn, ext)
+    if args.multi_kernel:
+        ext.set_option(_native.UQM_OPT_FUSED_DECODE, 0)
     shape = syn.CONFIGS[args.config]
     tokens = args.tokens if args.tokens > 0 else shape.tokens
     head = measure(torch, syn, ext, shape, tokens, args.steps, args.warmup, args.rotate_bytes)
@@ -441,7 +447,7 @@ def main() -> int:
     else:
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                    "traffic": profiled_traffic(shape.name) if tokens == 1 else None}
+                    "traffic": profiled_traffic(shape.name) if tokens == 1 and not args.multi_kernel else None}
     line = {
         "metric": BASELINE_METRIC,
         "value": round(us_per_layer / tokens, 3),
@@ -460,6 +466,7 @@ def main() -> int:
             "workload": workload_name(shape),
             "tokens": tokens,
             "rotated_instances": head["instances"],
+            "path": "multi-kernel" if args.multi_kernel or tokens > 2 else "fused",
             "parallelism": "single GPU",
         },
         "tokens_per_s": round(tokens / (us_per_layer * 1e-6), 1),
