@@ -372,3 +372,29 @@ def test_c3_stack_chain(hip_ext):
             x_g, _, weights, indices = hip_ext.moe_layer(layer, dense, n_g, shape.top_k)
             ref, *_ = om.qwen_block(n_g.cpu(), lay, reader, l, routes=(weights.cpu(), indices.cpu()))
             assert_close(x_g, ref, f"c3 chain step {step} layer {l}")
+
+
+def test_workspace_reused_across_token_counts(hip_ext):
+    """One zero-filled workspace serves calls of 1, 2, 32, 3 and 1 tokens in a
+    row (fused single-token launches, then the multi-launch path with the
+    side stream and the fused top-k + permutation): every call gives the same
+    bits as the same call on a fresh workspace, so the synchronisation words
+    each path leaves behind sit where the next token count looks for them."""
+    shape = syn.C2
+    note("workspace reuse across token counts")
+    layer = syn.build_experts(shape, device=DEV)
+    dense = syn.build_dense(shape, device=DEV)
+    counts = (1, 2, 32, 3, 1)
+
+    def ws_bytes(t):
+        return hip_ext.lib.uqm_moe_workspace_bytes(t, shape.hidden, shape.intermediate, shape.shared_intermediate,
+                                                   shape.num_experts, shape.top_k)
+
+    shared_ws = torch.zeros(max(ws_bytes(t) for t in counts), dtype=torch.uint8, device=DEV)
+    for i, t in enumerate(counts):
+        x = syn.hidden_states(shape, t, seed=90 + i).to(DEV)
+        got = [v.clone() for v in hip_ext.moe_layer(layer, dense, x, shape.top_k, workspace=shared_ws)]
+        fresh = torch.zeros(ws_bytes(t), dtype=torch.uint8, device=DEV)
+        ref = hip_ext.moe_layer(layer, dense, x, shape.top_k, workspace=fresh)
+        for a, b, what in zip(got, ref, ("out", "logits", "weights", "indices")):
+            assert torch.equal(a, b), f"t={t} {what}"
