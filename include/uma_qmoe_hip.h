@@ -58,8 +58,6 @@ enum { UQM_Q4 = 0, UQM_Q8 = 1, UQM_BF16 = 2 };
 enum {
   UQM_OPT_FUSED_DECODE = 1,   /* 1 (default): blocks of one or two tokens use the fused persistent
                                   kernel, one launch per token */
-  UQM_OPT_FUSED_ROUTED_BLOCKS = 2, /* accepted, no effect: every CU of the fused kernel takes a share
-                                      of every phase (values 0..4096 as before) */
   UQM_OPT_MFMA_MIN_TOKENS = 3,     /* token count from which multi-token calls run the expert projections
                                       as MFMA grouped GEMMs (default 2; 0 = never, batched GEMV instead) */
   UQM_OPT_OVERLAP_SHARED = 4       /* 1 (default): multi-token blocks run the shared expert on a
@@ -191,10 +189,13 @@ int uqm_norm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64
 int uqm_set_option(int option, int64_t value);
 
 /* Synchronously reads (and clears) the sticky error word that the fused
- * single-token kernel raises when one of its bounded inter-wave waits expires
- * (which can only happen when its grid is not fully resident, e.g. while
- * another persistent kernel holds the device). Returns UQM_OK when clean. No
- * counterpart in the reference. */
+ * single-token kernel raises when one of its inter-workgroup waits runs past
+ * its wall-clock budget (2 ms from the start of each wave; a launch takes
+ * ~20 us). That can only happen when its grid is not fully resident, e.g.
+ * while another kernel holds CUs. Such a launch still ends within the budget,
+ * and its output is poisoned rather than silently wrong: NaN output rows, and
+ * routes -1 / weights NaN when the routing itself expired. Returns UQM_OK when
+ * clean. No counterpart in the reference. */
 int uqm_workspace_status(void* workspace, size_t workspace_bytes, void* stream);
 
 /* RMSNorm (Transformers Qwen2MoeRMSNorm, modeling_qwen2_moe.py:65-70): bf16 in/out,

@@ -57,7 +57,7 @@ def header_enum_values() -> dict[str, int]:
 
 def test_python_constants_match_header_enums():
     values = header_enum_values()
-    for name in ("UQM_Q4", "UQM_Q8", "UQM_BF16", "UQM_OPT_FUSED_DECODE", "UQM_OPT_FUSED_ROUTED_BLOCKS",
+    for name in ("UQM_Q4", "UQM_Q8", "UQM_BF16", "UQM_OPT_FUSED_DECODE",
                  "UQM_OPT_MFMA_MIN_TOKENS", "UQM_OPT_OVERLAP_SHARED"):
         assert values[name] == getattr(_native, name), name
 

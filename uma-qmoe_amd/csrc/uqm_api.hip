@@ -87,7 +87,6 @@ P* at(void* ws, size_t off) {
 
 // Process-wide options (uqm_set_option).
 std::atomic<int64_t> g_opt_fused{1};
-std::atomic<int64_t> g_opt_fused_routed_blocks{0};
 std::atomic<int64_t> g_opt_mfma_min_tokens{2};
 std::atomic<int64_t> g_opt_overlap_shared{1};
 
@@ -108,6 +107,25 @@ int device_cus() {
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
   if (dev >= 0 && dev < 64) g_cus[dev].store(n, std::memory_order_relaxed);
   return n;
+}
+
+// The fused kernel's wait budget in s_memrealtime ticks of the current device
+// (cached per device id; the clock runs at hipDeviceAttributeWallClockRate kHz).
+std::atomic<int64_t> g_wait_ticks[64];
+
+uint64_t fused_wait_ticks() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  if (dev >= 0 && dev < 64) {
+    const int64_t v = g_wait_ticks[dev].load(std::memory_order_relaxed);
+    if (v > 0) return static_cast<uint64_t>(v);
+  }
+  int khz = 0;
+  if (dev < 0 || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0)
+    khz = 100000;  // the 100 MHz reference clock of CDNA parts
+  const int64_t ticks = static_cast<int64_t>(khz) * uqm::kFusedWaitBudgetUs / 1000;
+  if (dev >= 0 && dev < 64) g_wait_ticks[dev].store(ticks, std::memory_order_relaxed);
+  return static_cast<uint64_t>(ticks);
 }
 
 // Launch shape of one MFMA grouped GEMM (see launch_expert_mfma).
@@ -722,6 +740,7 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
     fa.k = static_cast<int>(k);
     fa.group = w->encoding == UQM_BF16 ? 1 : w->group_size;
     fa.norm = layer->norm_topk_prob;
+    fa.wait_ticks = fused_wait_ticks();
     fa.sync = at<uint32_t>(workspace, L.fused_sync);
     fa.hs = at<uint32_t>(workspace, L.fused_hs);
     fa.hr = at<uint32_t>(workspace, L.fused_hr);
@@ -870,10 +889,6 @@ int uqm_set_option(int option, int64_t value) {
   switch (option) {
     case UQM_OPT_FUSED_DECODE:
       g_opt_fused.store(value != 0 ? 1 : 0);
-      return UQM_OK;
-    case UQM_OPT_FUSED_ROUTED_BLOCKS:
-      if (value < 0 || value > 4096) return fail(UQM_ERR_ARGUMENT, "routed workgroups must be in [0, 4096]");
-      g_opt_fused_routed_blocks.store(value);
       return UQM_OK;
     case UQM_OPT_MFMA_MIN_TOKENS:
       if (value < 0) return fail(UQM_ERR_ARGUMENT, "token threshold must be >= 0");

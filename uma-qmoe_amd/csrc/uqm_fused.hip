@@ -32,9 +32,17 @@
 // reloads until every tag carries this launch's epoch; there are no counter
 // barriers and no store drains on the critical path. Each workgroup keeps its
 // own copy of the epoch in the workspace and advances it once per launch.
-// Every wait is bounded: when a bound expires the kernel raises a sticky error
-// word and still runs to the end, so no wave can hang the device. The waits
-// need all workgroups resident at once: the grid is one workgroup per CU.
+// The waits need all workgroups resident at once (the grid is one workgroup
+// per CU), and every wait is bounded by wall-clock time: each wave takes a
+// deadline (s_memrealtime, kFusedWaitBudgetUs) at its start, shared by all
+// of its waits. When one expires, the wave raises the sticky error word,
+// records the launch's epoch in the expired word (the product waits of every
+// other wave then give up at once) and runs to the end, so no wave can hang
+// the device and a launch that lost its co-residency ends within the budget.
+// Its result is poisoned, never silently wrong: routes taken from an
+// incomplete logit poll make the workgroup publish NaN products, and a wave
+// whose product staging expired writes NaN output rows (with routes -1 and
+// weights NaN from workgroup 0 when its own poll expired).
 //
 // Each lane streams fixed 16-byte column chunks of every row (non-temporal
 // loads: each weight byte is read once) against activation fragments held in
@@ -62,12 +70,12 @@ namespace {
 constexpr int kWaves = 8;                  // streaming waves per workgroup
 constexpr int kThreads = (kWaves + 1) * 64;  // + the control wave
 constexpr int kLdsHeader = 256;            // flags, routes, weights, shared gate (16-byte aligned)
-constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a wait gives up (well over 0.1 s)
+constexpr uint16_t kBf16NaN = 0x7FC0;      // poison of products and outputs after an expired wait
 constexpr int kPollSleep = 40;             // s_sleep units (64 clocks) between router logit polls
 constexpr int kPollDelay = 64;             // s_sleep units before the first poll (the logits cannot be
                                            // in sooner; fewer polls leave more bandwidth to phase A)
-constexpr int kRouterHeadStart = 12;
-enum { kNormNone = 0, kNormUnit = 1, kNormWeighted = 2 };  // input RMSNorm: none, weight ones, weight row       // s_sleep units the streaming waves of router workgroups yield
+constexpr int kRouterHeadStart = 12;       // s_sleep units the streaming waves of router workgroups yield
+enum { kNormNone = 0, kNormUnit = 1, kNormWeighted = 2 };  // input RMSNorm: none, weight ones, weight row
 #ifndef UQM_FUSED_CTRL_PRIO
 #define UQM_FUSED_CTRL_PRIO 3
 #endif
@@ -94,6 +102,20 @@ __device__ __forceinline__ void drain() {
 }
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Constant-rate wall clock (hipDeviceAttributeWallClockRate ticks).
+__device__ __forceinline__ uint64_t wall_clock() { return __builtin_amdgcn_s_memrealtime(); }
+
+// A wait of this wave expired: raise the sticky error word and mark the
+// launch (epoch) as expired, ordered before anything the workgroup publishes
+// afterwards.
+__device__ __forceinline__ void raise_expired(uint32_t* sync, uint32_t epoch) {
+  if ((threadIdx.x & 63) == 0) {
+    atomicOr(sync + kSyncError, 1u);
+    co_store<uint32_t>(sync + kSyncExpired, epoch);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+}
 
 template <int V>
 constexpr int log2_of() {
@@ -381,6 +403,8 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   int* l_route = reinterpret_cast<int*>(lds);
   float* l_w = reinterpret_cast<float*>(lds + 32);
   float* l_sg = reinterpret_cast<float*>(lds + 64);
+  int* l_bad = reinterpret_cast<int*>(lds + 96);     // routes came from an expired logit poll
+  int* l_stale = reinterpret_cast<int*>(lds + 100);  // a product staging wait expired
   uint16_t* lhs = reinterpret_cast<uint16_t*>(lds + kLdsHeader);
   uint16_t* lhr = lhs + Is;
   uint32_t* lfr = reinterpret_cast<uint32_t*>(lds + kLdsHeader + 2 * (Is + k * I));
@@ -393,7 +417,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   (void)gw;
   UQM_FUSED_TRACE_INIT
   UQM_FUSED_TRACE(0);
-  uint32_t* const error = a.sync + kSyncError;
+  const uint64_t deadline = wall_clock() + a.wait_ticks;
   uint32_t* const my_epoch = a.sync + kSyncEpochBase + b;
   const int group = ER::kScaled ? a.group : 1;
   const int nrow = E + (kShared ? 1 : 0);  // router rows + the shared-expert gate row
@@ -500,13 +524,15 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     poll(pb);
     __builtin_amdgcn_s_sleep(kPollSleep);
     poll(pc);
-    for (uint32_t round = 0;; ++round) {
+    bool bad = false;
+    for (;;) {
       if (ready(pa)) {
         take(pa);
         break;
       }
-      if (round > kSpinLimit / 4) {
-        if (lane == 0) atomicOr(error, 1u);
+      if (wall_clock() > deadline) {
+        raise_expired(a.sync, epoch);
+        bad = true;
         take(pa);
         break;
       }
@@ -562,10 +588,14 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     }
     float p = lane < k ? __expf(route_l - mx) / se : 0.f;
     if (a.norm) p = p / wave_sum(p);
-    const uint16_t wb = f32_to_bf16(p);
+    const uint16_t wb = bad ? kBf16NaN : f32_to_bf16(p);
     if (lane < k) {
       l_route[lane] = route_e;
       l_w[lane] = bf16_to_f32(wb);
+    }
+    if (lane == 0) {
+      *l_bad = bad ? 1 : 0;
+      *l_stale = 0;
     }
     if constexpr (kShared) {
       float le = 0.f;
@@ -578,7 +608,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     if (b == 0) {
       if (lane < k) {
         if (a.weights_out != nullptr) a.weights_out[lane] = wb;
-        if (a.indices_out != nullptr) a.indices_out[lane] = route_e;
+        if (a.indices_out != nullptr) a.indices_out[lane] = bad ? -1 : route_e;
       }
       if (a.logits_out != nullptr) {
 #pragma unroll
@@ -682,6 +712,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   // wave start phase B on its own, through an LDS flag, measured slower).
   lds_barrier();  // routes ready
   const int route_e = lane < k ? l_route[lane] : 0;
+  const bool routes_bad = *l_bad != 0;
   UQM_FUSED_TRACE(5);
 
   // Phase B: routed gate+up row pairs q = slot * I + i, RBP pairs per batch.
@@ -724,8 +755,10 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     constexpr int kL = log2_of<VB>();
     const int idx = lane >> (6 - kL);
     const int t = idx >> 1;
-    if ((lane & ((64 >> kL) - 1)) == 0 && (idx & 1) == 0 && t < n)
-      co_store<uint32_t>(a.hr + q0 + t, tag16(epoch_after(sum), f32_to_bf16(silu(round_bf16(sum)) * round_bf16(up))));
+    if ((lane & ((64 >> kL) - 1)) == 0 && (idx & 1) == 0 && t < n) {
+      const uint16_t h = routes_bad ? kBf16NaN : f32_to_bf16(silu(round_bf16(sum)) * round_bf16(up));
+      co_store<uint32_t>(a.hr + q0 + t, tag16(epoch_after(sum), h));
+    }
   };
 
   // Phase C: output rows o in [oa, ob): the shared down row (CISX chunks per
@@ -831,13 +864,21 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     }
     return __all(ok) != 0;
   };
+  // Retries give up at this wave's deadline, or at once when another wave
+  // has marked this launch as expired; the workgroup's outputs are then
+  // poisoned (l_stale).
   auto finish_round = [&](const uint64_t* src, int n2, int base, uint32_t* dst, uint64_t (&v)[SL]) {
     // The first check is outside the retry loop, so the compiler waits for
     // exactly these loads (not for the rows issued after them).
     if (!round_ok(n2, base, v)) {
-      for (uint32_t spins = 0;; ++spins) {
-        if (spins > kSpinLimit) {
-          if (lane == 0) atomicOr(error, 1u);
+      for (;;) {
+        if (wall_clock() > deadline) {
+          raise_expired(a.sync, epoch);
+          if (lane == 0) *l_stale = 1;
+          break;
+        }
+        if (co_load(a.sync + kSyncExpired) == epoch) {
+          if (lane == 0) *l_stale = 1;
           break;
         }
         __builtin_amdgcn_s_sleep(2);
@@ -925,10 +966,11 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   build_fragments();
   lds_barrier();  // routed fragments built
   UQM_FUSED_TRACE(8);
+  const bool stale = *l_stale != 0;
   // out[o] = bf16(sum over lanes of (shared part + routed part)).
   {
     const float y = wave_sum(acc_s + routed_part());
-    if (lane == 0 && oa < ob) a.out[oa] = f32_to_bf16(y);
+    if (lane == 0 && oa < ob) a.out[oa] = stale ? kBf16NaN : f32_to_bf16(y);
   }
   for (int o = oa + 1; o < ob; ++o) {  // more rows than streaming waves (small grids only)
     Cols<kBF16, CISX> cis;
@@ -936,7 +978,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     issue_cs(o, cis);
     issue_cr(o);
     const float y = wave_sum(shared_part(cis) + routed_part());
-    if (lane == 0) a.out[o] = f32_to_bf16(y);
+    if (lane == 0) a.out[o] = stale ? kBf16NaN : f32_to_bf16(y);
   }
   UQM_FUSED_TRACE(9);
 }

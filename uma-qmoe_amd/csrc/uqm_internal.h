@@ -123,9 +123,14 @@ hipError_t launch_combine(const float* y, int y_parts, int64_t y_stride, const u
                           int ys_parts, int64_t ys_stride, const float* sg, uint16_t* out, hipStream_t stream);
 // Single-token fused MoE block (uqm_fused.hip). Sync words live in `sync`
 // (zero before the first launch): a sticky error word the kernel raises when
-// one of its bounded waits expires, and one launch epoch per workgroup that
-// the workgroup advances on every launch.
-enum : int { kSyncError = 4, kSyncEpochBase = 64 };
+// one of its bounded waits expires (cleared only by uqm_workspace_status), the
+// epoch of the last launch in which a wait expired (the other waits of that
+// launch then give up at once), and one launch epoch per workgroup that the
+// workgroup advances on every launch.
+enum : int { kSyncError = 4, kSyncExpired = 5, kSyncEpochBase = 64 };
+// Wall-clock budget of one fused launch's waits, counted by every wave from
+// its own start (~20 us is a normal launch).
+constexpr int64_t kFusedWaitBudgetUs = 2000;
 constexpr int kMaxFusedBlocks = 1024;  // workgroups (one per CU)
 constexpr int kSyncWords = kSyncEpochBase + kMaxFusedBlocks;
 
@@ -147,6 +152,7 @@ struct FusedArgs {
   const float* eds;
   int64_t H, I, Is;
   int E, k, group, norm;
+  uint64_t wait_ticks;                 // wait budget in s_memrealtime ticks (kFusedWaitBudgetUs)
   uint32_t* sync;                      // kSyncWords words
   uint32_t* hs;                        // [Is] epoch-tagged shared SiLU products (8-byte aligned)
   uint32_t* hr;                        // [k, I] epoch-tagged routed SiLU products (8-byte aligned)

@@ -12,7 +12,8 @@ namespace uqm {
 // and put back to zero by the launch's last workgroup. Its offset does not
 // depend on the token count, so a workspace reused across token counts keeps it.
 constexpr int kSyncPermuteDone = 8;
-static_assert(kSyncPermuteDone != kSyncError && kSyncPermuteDone < kSyncEpochBase, "sync word taken");
+static_assert(kSyncPermuteDone != kSyncError && kSyncPermuteDone != kSyncExpired && kSyncPermuteDone < kSyncEpochBase,
+              "sync word taken");
 
 // Top-k (over bf16 logits, or over `parts` FP32 partials when plog is set)
 // and the permutation of its routes into rt, in one launch.

@@ -20,7 +20,6 @@ UQM_Q8 = 1
 UQM_BF16 = 2
 
 UQM_OPT_FUSED_DECODE = 1
-UQM_OPT_FUSED_ROUTED_BLOCKS = 2
 UQM_OPT_MFMA_MIN_TOKENS = 3
 UQM_OPT_OVERLAP_SHARED = 4
 
