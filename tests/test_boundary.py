@@ -22,7 +22,7 @@ from uma_qmoe_amd.custom_op import (
     unregister_expert_pack,
 )
 from uma_qmoe_amd.native_backend import MixedTargetNativeBackend, PackedQ4NativeBackend
-from uma_qmoe_amd.q4 import ContractError
+from uma_qmoe_amd.formats import ContractError
 
 
 class _Reader:
@@ -145,25 +145,42 @@ def _fake_ext(**names):
     return SimpleNamespace(**{n: (lambda *a: None) for n in names})
 
 
+Q4_EXT = dict(q4_linear=1, q4_moe_forward=1)
+
+
 def test_backend_requires_entry_points_and_platform():
-    with pytest.raises(ContractError, match="q4_moe_prefill"):
-        PackedQ4NativeBackend("hip_gfx950", _fake_ext(q4_linear=1, q4_moe_forward=1))
+    with pytest.raises(ContractError, match="q4_moe_forward"):
+        PackedQ4NativeBackend("hip_gfx950", _fake_ext(q4_linear=1))
     with pytest.raises(ContractError, match="q8_moe_forward"):
-        MixedTargetNativeBackend("hip_gfx950", _fake_ext(q4_linear=1, q4_moe_forward=1, q4_moe_prefill=1, q8_linear=1))
+        MixedTargetNativeBackend("hip_gfx950", _fake_ext(**Q4_EXT, q8_linear=1, bf16_linear=1))
     with pytest.raises(ContractError, match="platform"):
-        PackedQ4NativeBackend("hip_gfx1151", _fake_ext(q4_linear=1, q4_moe_forward=1, q4_moe_prefill=1))
+        PackedQ4NativeBackend("hip_gfx1151", _fake_ext(**Q4_EXT))
 
 
-def test_backend_releases_closed_pack_cache():
-    backend = PackedQ4NativeBackend("hip_gfx950", _fake_ext(q4_linear=1, q4_moe_forward=1, q4_moe_prefill=1))
-    backend._cache[(1, "first", "cuda:0")] = object()
-    backend._cache[(2, "second", "cuda:0")] = object()
-    backend._layer_cache[(1, 0, "cuda:0")] = object()
-    backend._layer_cache[(2, 0, "cuda:0")] = object()
+def _cpu_layer(experts=4, hidden=256, inter=128):
+    from uma_qmoe_amd import synthetic as syn
+
+    shape = syn.MoEShape("boundary_cache", hidden, experts, 2, inter)
+    return syn.build_experts(shape)
+
+
+def test_backend_cache_summary_and_release_by_pack():
+    backend = PackedQ4NativeBackend("hip_gfx950", _fake_ext(**Q4_EXT))
+    first, second = _cpu_layer(), _cpu_layer(experts=6)
+    single = ("q4_group128", torch.zeros(64, dtype=torch.uint8), torch.ones(1), (1, 128), 128)
+    backend._layer_cache[(1, 0, "cuda:0")] = first
+    backend._layer_cache[(2, 0, "cuda:0")] = second
+    backend._cache[(1, "w", "cuda:0")] = single
+    summary = backend.cache_summary()
+    # compressed bytes: Q4 data (1/2 byte per weight) + FP32 scales (1/32 byte per weight), nothing expanded
+    per_expert = 3 * 128 * 256 // 2 + 3 * 128 * 256 // 128 * 4
+    assert summary == {"tensor_count": 1 + 3 * (4 + 6), "device_storage_bytes": 64 + 4 + (4 + 6) * per_expert,
+                       "dequantized_weight_bytes": 0}
     backend.release_pack(1)
-    assert set(backend._cache) == {(2, "second", "cuda:0")}
-    assert set(backend._layer_cache) == {(2, 0, "cuda:0")}
-    assert backend.cache_summary()["dequantized_weight_bytes"] == 0 if not backend._layer_cache else True
+    assert set(backend._cache) == set() and set(backend._layer_cache) == {(2, 0, "cuda:0")}
+    assert backend.cache_summary()["device_storage_bytes"] == 6 * per_expert
+    backend.release_pack(2)
+    assert backend.cache_summary() == {"tensor_count": 0, "device_storage_bytes": 0, "dequantized_weight_bytes": 0}
 
 
 def test_unregister_releases_backend_caches():
@@ -177,14 +194,16 @@ def test_unregister_releases_backend_caches():
             released.append(handle)
 
     register_performance_backend("cpu", Backend())
-    handle = register_expert_pack(_Reader())
-    unregister_expert_pack(handle)
-    assert handle in released
-    custom_op._PERFORMANCE_BACKENDS.pop("cpu", None)
+    try:
+        handle = register_expert_pack(_Reader())
+        unregister_expert_pack(handle)
+        assert handle in released
+    finally:
+        custom_op.REGISTRY.uninstall("cpu")
 
 
 def test_mixed_backend_rejects_q4_only_backend_for_other_encodings():
-    backend = PackedQ4NativeBackend("hip_gfx950", _fake_ext(q4_linear=1, q4_moe_forward=1, q4_moe_prefill=1))
+    backend = PackedQ4NativeBackend("hip_gfx950", _fake_ext(**Q4_EXT))
     reader = SimpleNamespace(layer_encoding=lambda layer: "q8_group128")
     with pytest.raises(RuntimeError, match="install the mixed backend"):
         backend._device_layer(1, 0, "cuda:0", reader)

@@ -133,7 +133,7 @@ def test_q8_round_trip_and_absmax_code():
 
 # ---------------------------------------------------- product vs oracle ----
 def test_product_q4_codec_matches_oracle():
-    from uma_qmoe_amd import q4 as pq
+    from uma_qmoe_amd import formats as pq
 
     rng = np.random.default_rng(2)
     for n in (1, 5, 128, 129, 1000):
@@ -150,21 +150,21 @@ def test_product_q4_codec_matches_oracle():
 
 
 def test_product_bulk_torch_codecs_match_oracle():
-    from uma_qmoe_amd.q4 import pack_codes_tensor, quantize_groups_tensor
-    from uma_qmoe_amd.target_pack import encode_target_tensor, float32_to_bf16_bits
+    from uma_qmoe_amd.formats import bf16_words, encode_projection, encode_target_tensor
 
     g = torch.Generator().manual_seed(3)
     w = torch.randn(3, 8, 256, generator=g) * 0.02
+    d4, s4 = encode_projection(w, "q4_group128")
+    d8, s8 = encode_projection(w, "q8_group128")
     for e in range(3):
-        codes, scales = quantize_groups_tensor(w[e].reshape(1, -1), 7)
-        packed = pack_codes_tensor(codes).numpy().tobytes()
         ref_p, ref_s = oc.q4_quantize(w[e].numpy(), 128)
-        assert packed == ref_p and scales.numpy().astype("<f4").tobytes() == ref_s
-        codes8, scales8 = quantize_groups_tensor(w[e].reshape(1, -1), 127)
+        assert d4[e].numpy().tobytes() == ref_p and s4[e].numpy().astype("<f4").tobytes() == ref_s
         ref_q, ref_s8 = oc.q8_quantize(w[e].numpy(), 128)
-        assert codes8.numpy().tobytes() == ref_q and scales8.numpy().astype("<f4").tobytes() == ref_s8
+        assert d8[e].numpy().tobytes() == ref_q and s8[e].numpy().astype("<f4").tobytes() == ref_s8
         t8 = encode_target_tensor(w[e].numpy(), "q8_group128")
         assert t8.data == ref_q and t8.scales == ref_s8
-    f = w.reshape(-1).numpy()
-    assert np.array_equal(float32_to_bf16_bits(f), oc.f32_to_bf16_bits(f))
-    assert np.array_equal(float32_to_bf16_bits(f), w.reshape(-1).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16))
+    f = w.reshape(-1)
+    assert np.array_equal(bf16_words(f).numpy().view(np.uint16), oc.f32_to_bf16_bits(f.numpy()))
+    db, sb = encode_projection(w, "bf16_le")
+    assert sb is None and np.array_equal(db.view(torch.int16).numpy().view(np.uint16).reshape(-1),
+                                         oc.f32_to_bf16_bits(f.numpy()))

@@ -21,7 +21,8 @@ import torch.nn.functional as F
 
 from oracle import codec as oc
 from oracle import moe as om
-from uma_qmoe_amd.target_pack import encode_target_tensor, memory_pack
+from uma_qmoe_amd.formats import encode_target_tensor
+from uma_qmoe_amd.packfile import memory_pack
 
 H, I, IS, E, K = 128, 64, 96, 8, 2
 

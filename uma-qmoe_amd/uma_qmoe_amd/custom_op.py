@@ -1,176 +1,225 @@
 """PyTorch operator boundary for packed-expert MoE execution on MI355X.
 
-Keeps the reference's operator contract (src/uma_qmoe/custom_op.py):
-  * schemas ``uma_qmoe::moe_forward`` and ``uma_qmoe::qwen_moe_forward``
+The contract kept from the reference (src/uma_qmoe/custom_op.py):
+  * op schemas ``uma_qmoe::moe_forward`` and ``uma_qmoe::qwen_moe_forward``
     (Tensor hidden_states, Tensor expert_indices, Tensor routing_weights,
     int layer_index, int pack_handle, bool performance_mode=False) -> Tensor,
     implemented for the CPU, CUDA (HIP builds of torch use this key) and Meta
-    dispatch keys (custom_op.py:582-628);
-  * pack handles with thread-local re-entrant leases; unregister drains active
-    calls and refuses inside its own lease (custom_op.py:51-146);
-  * explicit install-then-select performance backends; performance mode with
-    no backend fails closed (custom_op.py:90-100, 509-579).
+    dispatch keys, registered once (custom_op.py:582-628);
+  * integer pack handles from ``register_expert_pack`` /
+    ``register_target_pack`` for readers with exactly one mapping; leases
+    that are re-entrant per thread; ``unregister_expert_pack`` refuses inside
+    the caller's own lease, waits for other active calls and then makes the
+    installed backends release their device copies (custom_op.py:51-146);
+  * explicit install-then-select performance backends per platform, and a
+    performance-mode call without one fails closed with "silent reference
+    fallback is forbidden" (custom_op.py:90-100, 509-579).
 
-New in this build:
-  * ``uma_qmoe::moe_block`` — the whole MoE block (router + routed experts +
-    optional sigmoid-gated shared expert) as one op, so the router and shared
-    expert run in the same HIP pipeline instead of separate torch modules.
-  * The platform id of MI355X is ``hip_gfx950``.
-  * The correctness mode (performance_mode=False) runs an explicitly
-    registered correctness implementation (``register_reference_implementation``).
-    None ships with the product; without one the call raises instead of
-    computing anything on a fallback path.
+Different here:
+  * ``uma_qmoe::moe_block`` runs the whole MoE block (router, routed experts,
+    sigmoid-gated shared expert) as one op, so the router and the shared
+    expert run in the same HIP pipeline;
+  * the MI355X platform is ``hip_gfx950``;
+  * performance_mode=False runs an explicitly registered correctness
+    implementation (``register_reference_implementation``); none ships with
+    the product, so without one the call raises. The reference instead
+    computes its streaming correctness path there (custom_op.py:509-579).
 """
 
 from __future__ import annotations
 
+from collections import Counter
 from contextlib import contextmanager
 from dataclasses import dataclass
 import itertools
 import threading
 from typing import Any, Callable, Iterator
 
-from .q4 import ContractError
+from .formats import ContractError
 
 PLATFORMS = frozenset({"cpu", "hip_gfx950"})
+REFERENCE_KINDS = frozenset({"olmoe", "qwen", "block"})
 
 
 @dataclass
-class _PackState:
+class _Pack:
     reader: Any
-    active_calls: int = 0
+    active: int = 0  # calls (threads) holding a lease
     closing: bool = False
 
 
-_PACKS: dict[int, _PackState] = {}
-_PACK_CONDITION = threading.Condition()
-_PACK_IDS = itertools.count(1)
-_PACK_LEASES = threading.local()
-_LIBRARIES: list[Any] = []
-_REGISTERED = False
-_PERFORMANCE_BACKENDS: dict[str, Any] = {}
-_REFERENCE_IMPLEMENTATIONS: dict[str, Callable[..., Any]] = {}
+class PackRegistry:
+    """Registered pack readers, the per-thread leases on them, and the
+    backends that hold device copies of their tensors.
+
+    A lease counts once per thread however deeply it nests. Closing a handle
+    refuses new leases from other calls, waits until the active ones end,
+    forgets the handle and asks every installed backend to release it.
+    """
+
+    def __init__(self) -> None:
+        self._cond = threading.Condition()
+        self._ids = itertools.count(1)
+        self._packs: dict[int, _Pack] = {}
+        self._tls = threading.local()
+        self.backends: dict[str, Any] = {}
+        self.references: dict[str, Callable[..., Any]] = {}
+
+    def held(self) -> Counter:
+        """This thread's lease depth per handle."""
+        depth = getattr(self._tls, "depth", None)
+        if depth is None:
+            depth = self._tls.depth = Counter()
+        return depth
+
+    def register(self, reader: Any) -> int:
+        if getattr(reader, "mapping_count", None) != 1:
+            raise ContractError("custom operator requires exactly one ExpertPack mapping")
+        with self._cond:
+            handle = next(self._ids)
+            self._packs[handle] = _Pack(reader)
+            return handle
+
+    @contextmanager
+    def lease(self, handle: int) -> Iterator[Any]:
+        depth = self.held()
+        outer = depth[handle] == 0
+        with self._cond:
+            pack = self._packs.get(handle)
+            if pack is None or (pack.closing and outer):
+                raise RuntimeError(f"unknown or closed ExpertPack handle {handle}")
+            if outer:
+                pack.active += 1
+            depth[handle] += 1
+        try:
+            yield pack.reader
+        finally:
+            with self._cond:
+                depth[handle] -= 1
+                if depth[handle] == 0:
+                    del depth[handle]
+                    pack.active -= 1
+                    self._cond.notify_all()
+
+    def resolve(self, handle: int) -> Any:
+        if self.held()[handle] == 0:
+            raise RuntimeError("ExpertPack access requires an active operator lease")
+        with self._cond:
+            pack = self._packs.get(handle)
+            if pack is None:
+                raise RuntimeError(f"unknown or closed ExpertPack handle {handle}")
+            return pack.reader
+
+    def close(self, handle: int) -> None:
+        if self.held()[handle]:
+            raise ContractError("cannot unregister an ExpertPack from its active call")
+        with self._cond:
+            pack = self._packs.get(handle)
+            if pack is None:
+                return
+            if pack.closing:  # another thread is closing it: wait for that
+                self._cond.wait_for(lambda: handle not in self._packs)
+                return
+            pack.closing = True
+            self._cond.wait_for(lambda: pack.active == 0)
+            del self._packs[handle]
+            backends = list(self.backends.values())
+            self._cond.notify_all()
+        for backend in backends:
+            release = getattr(backend, "release_pack", None)
+            if callable(release):
+                release(handle)
+
+    def install(self, platform: str, backend: Any) -> None:
+        if platform not in PLATFORMS:
+            raise ContractError(f"unsupported custom operator platform {platform!r}")
+        if not callable(backend):
+            raise ContractError("custom operator backend must be callable")
+        with self._cond:
+            self.backends[platform] = backend
+
+    def backend(self, platform: str) -> Any:
+        with self._cond:
+            return self.backends.get(platform)
+
+    def uninstall(self, platform: str) -> None:
+        with self._cond:
+            self.backends.pop(platform, None)
+
+    def set_reference(self, kind: str, implementation: Callable[..., Any]) -> None:
+        if kind not in REFERENCE_KINDS:
+            raise ContractError(f"unknown reference implementation kind {kind!r}")
+        if not callable(implementation):
+            raise ContractError("reference implementation must be callable")
+        with self._cond:
+            self.references[kind] = implementation
+
+    def reference(self, kind: str) -> Callable[..., Any]:
+        with self._cond:
+            impl = self.references.get(kind)
+        if impl is None:
+            raise RuntimeError(f"uma_qmoe correctness mode has no registered {kind} implementation; "
+                               "pass performance_mode=True to run the HIP backend")
+        return impl
 
 
+REGISTRY = PackRegistry()
+
+
+# Reference-named entry points (src/uma_qmoe/custom_op.py:51-146).
 def register_expert_pack(reader: Any) -> int:
-    """Register one pack reader (exactly one mapping) and return its handle."""
-    if getattr(reader, "mapping_count", None) != 1:
-        raise ContractError("custom operator requires exactly one ExpertPack mapping")
-    with _PACK_CONDITION:
-        handle = next(_PACK_IDS)
-        _PACKS[handle] = _PackState(reader=reader)
-    return handle
+    """Register one pack reader (exactly one mapping); returns its handle."""
+    return REGISTRY.register(reader)
 
 
 def register_target_pack(reader: Any) -> int:
     """Register one mixed TargetPack (same contract as register_expert_pack)."""
-    return register_expert_pack(reader)
-
-
-def _lease_counts() -> dict[int, int]:
-    counts = getattr(_PACK_LEASES, "counts", None)
-    if counts is None:
-        counts = {}
-        _PACK_LEASES.counts = counts
-    return counts
+    return REGISTRY.register(reader)
 
 
 def unregister_expert_pack(handle: int) -> None:
-    """Close a handle: wait for active calls to drain, then release backends' caches."""
-    if _lease_counts().get(handle, 0):
-        raise ContractError("cannot unregister an ExpertPack from its active call")
-    with _PACK_CONDITION:
-        state = _PACKS.get(handle)
-        if state is None:
-            return
-        if state.closing:
-            while handle in _PACKS:
-                _PACK_CONDITION.wait()
-            return
-        state.closing = True
-        while state.active_calls:
-            _PACK_CONDITION.wait()
-        del _PACKS[handle]
-        backends = list(_PERFORMANCE_BACKENDS.values())
-        _PACK_CONDITION.notify_all()
-    for backend in backends:
-        release = getattr(backend, "release_pack", None)
-        if callable(release):
-            release(handle)
-
-
-def register_performance_backend(platform: str, implementation: Any) -> None:
-    """Install an explicit optimised backend; it is never an implicit fallback."""
-    if platform not in PLATFORMS:
-        raise ContractError(f"unsupported custom operator platform {platform!r}")
-    if not callable(implementation):
-        raise ContractError("custom operator backend must be callable")
-    with _PACK_CONDITION:
-        _PERFORMANCE_BACKENDS[platform] = implementation
-
-
-def performance_backend(platform: str) -> Any:
-    with _PACK_CONDITION:
-        return _PERFORMANCE_BACKENDS.get(platform)
-
-
-def register_reference_implementation(kind: str, implementation: Callable[..., Any]) -> None:
-    """Install the correctness implementation used when performance_mode=False.
-
-    ``kind`` is ``"olmoe"``, ``"qwen"`` or ``"block"``. The callable receives
-    the op's tensors plus the leased pack reader.
-    """
-    if kind not in {"olmoe", "qwen", "block"}:
-        raise ContractError(f"unknown reference implementation kind {kind!r}")
-    if not callable(implementation):
-        raise ContractError("reference implementation must be callable")
-    with _PACK_CONDITION:
-        _REFERENCE_IMPLEMENTATIONS[kind] = implementation
-
-
-def clear_reference_implementations() -> None:
-    with _PACK_CONDITION:
-        _REFERENCE_IMPLEMENTATIONS.clear()
+    """Close a handle once its active calls drain; backends drop its tensors."""
+    REGISTRY.close(handle)
 
 
 @contextmanager
 def acquire_expert_pack(handle: int) -> Iterator[Any]:
     """Hold one pack open across staging and asynchronous kernel submission."""
-    counts = _lease_counts()
-    nested = counts.get(handle, 0) > 0
-    with _PACK_CONDITION:
-        state = _PACKS.get(handle)
-        if state is None or (state.closing and not nested):
-            raise RuntimeError(f"unknown or closed ExpertPack handle {handle}")
-        if not nested:
-            state.active_calls += 1
-        counts[handle] = counts.get(handle, 0) + 1
-    try:
-        yield state.reader
-    finally:
-        with _PACK_CONDITION:
-            left = counts[handle] - 1
-            if left:
-                counts[handle] = left
-            else:
-                del counts[handle]
-                state.active_calls -= 1
-                _PACK_CONDITION.notify_all()
+    with REGISTRY.lease(handle) as reader:
+        yield reader
 
 
 def expert_pack_for_handle(handle: int) -> Any:
-    """Resolve a registered pack; only valid inside an active lease."""
-    if _lease_counts().get(handle, 0) == 0:
-        raise RuntimeError("ExpertPack access requires an active operator lease")
-    with _PACK_CONDITION:
-        state = _PACKS.get(handle)
-        if state is None:
-            raise RuntimeError(f"unknown or closed ExpertPack handle {handle}")
-        return state.reader
+    """The registered reader of a handle; only inside an active lease."""
+    return REGISTRY.resolve(handle)
+
+
+def register_performance_backend(platform: str, implementation: Any) -> None:
+    """Install an explicit optimised backend; it is never an implicit fallback."""
+    REGISTRY.install(platform, implementation)
+
+
+def performance_backend(platform: str) -> Any:
+    return REGISTRY.backend(platform)
+
+
+def register_reference_implementation(kind: str, implementation: Callable[..., Any]) -> None:
+    """Install the correctness implementation of performance_mode=False.
+
+    ``kind`` is ``"olmoe"`` (moe_forward), ``"qwen"`` (qwen_moe_forward) or
+    ``"block"`` (moe_block). It is called with the op's arguments, the pack
+    handle replaced by the leased reader.
+    """
+    REGISTRY.set_reference(kind, implementation)
+
+
+def clear_reference_implementations() -> None:
+    with REGISTRY._cond:
+        REGISTRY.references.clear()
 
 
 def device_platform(torch: Any, tensor: Any) -> str:
-    """``cpu`` or ``hip_gfx950``; anything else is rejected (custom_op.py:149-169)."""
+    """``cpu`` or ``hip_gfx950``; any other device is rejected (custom_op.py:149-169)."""
     if tensor.device.type == "cpu":
         return "cpu"
     if tensor.device.type != "cuda":
@@ -183,137 +232,92 @@ def device_platform(torch: Any, tensor: Any) -> str:
     return "hip_gfx950"
 
 
-def _reference(kind: str) -> Callable[..., Any]:
-    with _PACK_CONDITION:
-        impl = _REFERENCE_IMPLEMENTATIONS.get(kind)
-    if impl is None:
-        raise RuntimeError(
-            f"uma_qmoe correctness mode has no registered {kind} implementation; "
-            "pass performance_mode=True to run the HIP backend"
-        )
-    return impl
+# What each op runs in performance mode: the backend attribute (None: the
+# backend object itself) and the words of its fail-closed error.
+_OPS = {
+    "olmoe": (None, "registered"),
+    "qwen": ("qwen_forward", "Qwen-capable"),
+    "block": ("moe_block", "block-capable"),
+}
+
+
+def _run(kind: str, hidden_states: Any, args: tuple, pack_handle: int, performance_mode: bool) -> Any:
+    import torch
+
+    with REGISTRY.lease(pack_handle) as reader:
+        platform = device_platform(torch, hidden_states)
+        if not performance_mode:
+            return REGISTRY.reference(kind)(hidden_states, *args, reader)
+        attr, words = _OPS[kind]
+        backend = REGISTRY.backend(platform)
+        fn = backend if attr is None else getattr(backend, attr, None)
+        if fn is None or not callable(fn):
+            raise RuntimeError(f"performance mode has no {words} {platform} backend; "
+                               "silent reference fallback is forbidden")
+        return fn(hidden_states, *args, pack_handle)
 
 
 def _dispatch(hidden_states, expert_indices, routing_weights, layer_index, pack_handle, performance_mode=False):
-    import torch
-
-    with acquire_expert_pack(pack_handle) as reader:
-        platform = device_platform(torch, hidden_states)
-        if performance_mode:
-            backend = performance_backend(platform)
-            if backend is None:
-                raise RuntimeError(
-                    f"performance mode has no registered {platform} backend; silent reference fallback is forbidden"
-                )
-            return backend(hidden_states, expert_indices, routing_weights, layer_index, pack_handle)
-        return _reference("olmoe")(hidden_states, expert_indices, routing_weights, layer_index, reader)
+    return _run("olmoe", hidden_states, (expert_indices, routing_weights, layer_index), pack_handle, performance_mode)
 
 
 def _qwen_dispatch(hidden_states, expert_indices, routing_weights, layer_index, pack_handle, performance_mode=False):
+    return _run("qwen", hidden_states, (expert_indices, routing_weights, layer_index), pack_handle, performance_mode)
+
+
+def _block_dispatch(hidden_states, router_weight, shared_gate_proj, shared_up_proj, shared_down_proj,
+                    shared_expert_gate, top_k, norm_topk_prob, layer_index, pack_handle, performance_mode=False):
+    args = (router_weight, shared_gate_proj, shared_up_proj, shared_down_proj, shared_expert_gate, top_k,
+            norm_topk_prob, layer_index)
+    return _run("block", hidden_states, args, pack_handle, performance_mode)
+
+
+def _same_shape(hidden_states, *_rest):
+    return hidden_states.new_empty(hidden_states.shape)
+
+
+def _block_meta(hidden_states, router_weight, *rest):
     import torch
 
-    with acquire_expert_pack(pack_handle) as reader:
-        platform = device_platform(torch, hidden_states)
-        if performance_mode:
-            qwen_forward = getattr(performance_backend(platform), "qwen_forward", None)
-            if not callable(qwen_forward):
-                raise RuntimeError(
-                    f"performance mode has no Qwen-capable {platform} backend; silent reference fallback is forbidden"
-                )
-            return qwen_forward(hidden_states, expert_indices, routing_weights, layer_index, pack_handle)
-        return _reference("qwen")(hidden_states, expert_indices, routing_weights, layer_index, reader)
+    top_k = rest[4]
+    t = hidden_states.reshape(-1, hidden_states.shape[-1]).shape[0]
+    return (hidden_states.new_empty(hidden_states.shape), hidden_states.new_empty((t, router_weight.shape[0])),
+            hidden_states.new_empty((t, top_k)), hidden_states.new_empty((t, top_k), dtype=torch.int64))
 
 
-def _block_dispatch(
-    hidden_states,
-    router_weight,
-    shared_gate_proj,
-    shared_up_proj,
-    shared_down_proj,
-    shared_expert_gate,
-    top_k,
-    norm_topk_prob,
-    layer_index,
-    pack_handle,
-    performance_mode=False,
-):
-    import torch
-
-    args = (
-        hidden_states,
-        router_weight,
-        shared_gate_proj,
-        shared_up_proj,
-        shared_down_proj,
-        shared_expert_gate,
-        top_k,
-        norm_topk_prob,
-        layer_index,
-        pack_handle,
-    )
-    with acquire_expert_pack(pack_handle) as reader:
-        platform = device_platform(torch, hidden_states)
-        if performance_mode:
-            block = getattr(performance_backend(platform), "moe_block", None)
-            if not callable(block):
-                raise RuntimeError(
-                    f"performance mode has no block-capable {platform} backend; silent reference fallback is forbidden"
-                )
-            return block(*args)
-        return _reference("block")(*args[:-1], reader)
-
-
-def _block_meta(hidden_states, router_weight, *_rest):
-    top_k = _rest[4]
-    flat = hidden_states.reshape(-1, hidden_states.shape[-1])
-    t = flat.shape[0]
-    e = router_weight.shape[0]
-    return (
-        hidden_states.new_empty(hidden_states.shape),
-        hidden_states.new_empty((t, e)),
-        hidden_states.new_empty((t, top_k)),
-        hidden_states.new_empty((t, top_k), dtype=__import__("torch").int64),
-    )
+_SCHEMAS = {
+    "moe_forward": ("(Tensor hidden_states, Tensor expert_indices, Tensor routing_weights, int layer_index, "
+                    "int pack_handle, bool performance_mode=False) -> Tensor", _dispatch, _same_shape),
+    "qwen_moe_forward": ("(Tensor hidden_states, Tensor expert_indices, Tensor routing_weights, int layer_index, "
+                         "int pack_handle, bool performance_mode=False) -> Tensor", _qwen_dispatch, _same_shape),
+    "moe_block": ("(Tensor hidden_states, Tensor router_weight, Tensor? shared_gate_proj, Tensor? shared_up_proj, "
+                  "Tensor? shared_down_proj, Tensor? shared_expert_gate, int top_k, bool norm_topk_prob, "
+                  "int layer_index, int pack_handle, bool performance_mode=False) -> (Tensor, Tensor, Tensor, Tensor)",
+                  _block_dispatch, _block_meta),
+}
+_LIBRARIES: list[Any] = []
 
 
 def register_moe_forward() -> None:
-    """Register the uma_qmoe ops once (idempotent, under the registry lock)."""
-    global _REGISTERED
-    with _PACK_CONDITION:
-        if _REGISTERED:
+    """Define and implement the uma_qmoe ops once (idempotent, under a lock)."""
+    with REGISTRY._cond:
+        if _LIBRARIES:
             return
         import torch
 
-        definition = torch.library.Library("uma_qmoe", "DEF")
-        definition.define(
-            "moe_forward(Tensor hidden_states, Tensor expert_indices, Tensor routing_weights, "
-            "int layer_index, int pack_handle, bool performance_mode=False) -> Tensor"
-        )
-        definition.define(
-            "qwen_moe_forward(Tensor hidden_states, Tensor expert_indices, Tensor routing_weights, "
-            "int layer_index, int pack_handle, bool performance_mode=False) -> Tensor"
-        )
-        definition.define(
-            "moe_block(Tensor hidden_states, Tensor router_weight, Tensor? shared_gate_proj, "
-            "Tensor? shared_up_proj, Tensor? shared_down_proj, Tensor? shared_expert_gate, int top_k, "
-            "bool norm_topk_prob, int layer_index, int pack_handle, bool performance_mode=False) "
-            "-> (Tensor, Tensor, Tensor, Tensor)"
-        )
-        for key in ("CPU", "CUDA"):
-            impl = torch.library.Library("uma_qmoe", "IMPL", key)
-            impl.impl("moe_forward", _dispatch)
-            impl.impl("qwen_moe_forward", _qwen_dispatch)
-            impl.impl("moe_block", _block_dispatch)
-            _LIBRARIES.append(impl)
-        meta = torch.library.Library("uma_qmoe", "IMPL", "Meta")
-        meta.impl("moe_forward", lambda hidden_states, *_a: hidden_states.new_empty(hidden_states.shape))
-        meta.impl("qwen_moe_forward", lambda hidden_states, *_a: hidden_states.new_empty(hidden_states.shape))
-        meta.impl("moe_block", _block_meta)
-        _LIBRARIES.extend((definition, meta))
-        _REGISTERED = True
+        libs = {key: torch.library.Library("uma_qmoe", kind, *(() if key == "DEF" else (key,)))
+                for key, kind in (("DEF", "DEF"), ("CPU", "IMPL"), ("CUDA", "IMPL"), ("Meta", "IMPL"))}
+        for name, (schema, impl, meta) in _SCHEMAS.items():
+            libs["DEF"].define(name + schema)
+            libs["CPU"].impl(name, impl)
+            libs["CUDA"].impl(name, impl)
+            libs["Meta"].impl(name, meta)
+        _LIBRARIES.extend(libs.values())
 
 
 __all__ = [
+    "REGISTRY",
+    "PackRegistry",
     "acquire_expert_pack",
     "clear_reference_implementations",
     "device_platform",

@@ -33,7 +33,7 @@ from typing import Any
 from . import _native
 from .build import CSRC
 from .custom_op import acquire_expert_pack, register_performance_backend
-from .q4 import ContractError
+from .formats import ENCODINGS, ContractError
 
 EXPERT_NAME = "model.layers.{layer}.mlp.experts.{expert}.{proj}.weight"
 PROJECTIONS = ("gate_proj", "up_proj", "down_proj")
@@ -363,29 +363,24 @@ class HipExtension:
 
     def q4_moe_forward(self, hidden, indices, weights, gate_packed, gate_scales, up_packed, up_scales, down_packed,
                        down_scales, group_size, *, num_experts=None):
+        """Routed experts of any token count (the route permutation is built
+        on the device; packed_q4_binding.cpp:197-347 took host-built tables
+        for prefill)."""
         return self._fixed("q4_group128", hidden, indices, weights, gate_packed, gate_scales, up_packed, up_scales,
                            down_packed, down_scales, group_size, num_experts)
-
-    def q4_moe_prefill(self, hidden, indices, weights, route_order, expert_offsets, gate_packed, gate_scales,
-                       up_packed, up_scales, down_packed, down_scales, group_size, *, num_experts=None):
-        # The route permutation is rebuilt on the device; the host's tensors are
-        # accepted for signature compatibility and checked for shape only.
-        if route_order.numel() != indices.numel():
-            raise RuntimeError("route_order must hold one entry per route")
-        return self.q4_moe_forward(hidden, indices, weights, gate_packed, gate_scales, up_packed, up_scales,
-                                   down_packed, down_scales, group_size, num_experts=num_experts)
 
     def q8_moe_forward(self, hidden, indices, weights, gate_q, gate_scales, up_q, up_scales, down_q, down_scales,
                        group_size, *, num_experts=None):
         return self._fixed("q8_group128", hidden, indices, weights, gate_q, gate_scales, up_q, up_scales, down_q,
                            down_scales, group_size, num_experts)
 
-    def q8_moe_prefill(self, hidden, indices, weights, route_order, expert_offsets, gate_q, gate_scales, up_q,
-                       up_scales, down_q, down_scales, group_size, *, num_experts=None):
-        if route_order.numel() != indices.numel():
-            raise RuntimeError("route_order must hold one entry per route")
-        return self.q8_moe_forward(hidden, indices, weights, gate_q, gate_scales, up_q, up_scales, down_q, down_scales,
-                                   group_size, num_experts=num_experts)
+    def status(self) -> None:
+        """Raises if a fused launch on any workspace this extension holds hit
+        its wait budget (synchronises each workspace's stream)."""
+        with self._ws_lock:
+            spaces = list(self._ws_cache.values())
+        for ws in spaces:
+            self.workspace_status(ws)
 
 
 def load_native_extension(*, build_directory: str | Path | None = None, verbose: bool = False) -> tuple[str, HipExtension]:
@@ -413,25 +408,33 @@ def load_native_extension(*, build_directory: str | Path | None = None, verbose:
 
 
 # --------------------------------------------------------------- staging --
-def _pack_num_experts(reader: Any, layer_index: int) -> int:
+_NP_DTYPE = {"q4_group128": "u1", "q8_group128": "i1", "bf16_le": "<u2"}
+
+
+def _release(*views: Any) -> None:
+    for v in views:
+        release = getattr(v, "release", None)
+        if callable(release):
+            release()
+
+
+def layer_expert_count(reader: Any, layer_index: int) -> int:
+    """E of one layer: the fixed model's expert count when the pack names its
+    model, else the experts 0..E-1 whose gate projection the pack holds."""
     header = getattr(reader, "header", None)
     model = header.get("model", {}) if isinstance(header, dict) else {}
     if "num_experts" in model:
         return int(model["num_experts"])
-    e = 0
-    while True:
-        try:
-            views = reader.tensor_views(EXPERT_NAME.format(layer=layer_index, expert=e, proj="gate_proj"))
-        except (KeyError, ValueError, RuntimeError):
-            break
-        for v in views[:2]:
-            release = getattr(v, "release", None)
-            if callable(release):
-                release()
-        e += 1
-    if e == 0:
-        raise RuntimeError(f"pack has no experts for layer {layer_index}")
-    return e
+    names = getattr(reader, "names", None)
+    if callable(names):
+        prefix = f"model.layers.{layer_index}.mlp.experts."
+        ids = {int(n[len(prefix):].split(".", 1)[0]) for n in names()
+               if n.startswith(prefix) and n.endswith(".gate_proj.weight")}
+        if ids and ids == set(range(len(ids))):
+            return len(ids)
+        if ids:
+            raise RuntimeError(f"layer {layer_index} experts are not numbered 0..E-1")
+    raise RuntimeError(f"pack has no experts for layer {layer_index}")
 
 
 def _layer_encoding(reader: Any, layer_index: int) -> str:
@@ -439,71 +442,96 @@ def _layer_encoding(reader: Any, layer_index: int) -> str:
     return getter(layer_index) if callable(getter) else "q4_group128"
 
 
-def stage_experts(reader: Any, layer_index: int, device: Any, num_experts: int | None = None) -> DeviceExperts:
+class PinnedStaging:
+    """A grow-only pinned host buffer: expert tensors are gathered into it
+    from the pack's (memory-mapped) views and reach the device in one DMA per
+    projection."""
+
+    def __init__(self) -> None:
+        self._buf = None
+        self.lock = threading.Lock()
+
+    def take(self, nbytes: int, pinned: bool = True):
+        import torch
+
+        if not pinned:  # staging for a host-memory destination
+            return torch.empty(nbytes, dtype=torch.uint8)
+        if self._buf is None or self._buf.numel() < nbytes:
+            self._buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, pin_memory=True)
+        return self._buf[:nbytes]
+
+
+_STAGING = PinnedStaging()
+
+
+def stage_experts(reader: Any, layer_index: int, device: Any, num_experts: int | None = None,
+                  staging: PinnedStaging | None = None) -> DeviceExperts:
     """Copy one layer's compressed experts to the device, expert-major.
 
-    Follows _host_projection / _device_layer (src/uma_qmoe/native_backend.py:
-    374-455, 769-842): concatenate experts 0..E-1 of each projection, check
-    that every expert has the same shape, one host-to-device copy each.
+    The staged layout is the reference's (_host_projection / _device_layer,
+    src/uma_qmoe/native_backend.py:374-455, 769-842): projection by
+    projection, experts 0..E-1 concatenated, every expert of one shape. The
+    bytes go from the reader's views into a pinned buffer and from there to
+    the device in one copy per tensor kind, nothing is expanded.
     """
     import numpy as np
     import torch
 
     encoding = _layer_encoding(reader, layer_index)
-    if num_experts is None:
-        num_experts = _pack_num_experts(reader, layer_index)
-    dtype_np = {"q4_group128": np.uint8, "q8_group128": np.int8, "bf16_le": np.uint16}[encoding]
-    staged: dict[str, tuple[Any, Any]] = {}
+    if encoding not in ENCODINGS:
+        raise RuntimeError(f"layer {layer_index} has unsupported encoding {encoding!r}")
+    E = layer_expert_count(reader, layer_index) if num_experts is None else int(num_experts)
+    stg = staging or _STAGING
+    dev = torch.device(device)
+    out: dict[str, tuple[Any, Any]] = {}
     shapes: dict[str, tuple[int, int]] = {}
     group = 128
-    for proj in PROJECTIONS:
-        datas, scales = [], []
-        shape = None
-        for e in range(num_experts):
-            name = EXPERT_NAME.format(layer=layer_index, expert=e, proj=proj)
-            data_view, scale_view, meta = reader.tensor_views(name)
+    with stg.lock:
+        for proj in PROJECTIONS:
+            views = []
             try:
-                if meta.get("encoding", encoding) != encoding:
-                    raise RuntimeError(f"tensor {name!r} is {meta.get('encoding')}, layer {layer_index} is {encoding}")
-                s = tuple(int(v) for v in meta["shape"])
-                if len(s) != 2:
-                    raise RuntimeError(f"expert tensor {name!r} is not a matrix")
-                if shape is None:
-                    shape = s
-                elif s != shape:
-                    raise RuntimeError(f"expert tensor {name!r} has unexpected shape {s!r}")
-                if meta.get("group_size"):
-                    group = int(meta["group_size"])
-                datas.append(np.frombuffer(data_view, dtype=dtype_np).copy())
-                if encoding != "bf16_le":
-                    scales.append(np.frombuffer(scale_view, dtype="<f4").copy())
+                for e in range(E):
+                    name = EXPERT_NAME.format(layer=layer_index, expert=e, proj=proj)
+                    data, scales, meta = reader.tensor_views(name)
+                    views.append((data, scales))
+                    if meta.get("encoding", encoding) != encoding:
+                        raise RuntimeError(f"tensor {name!r} is {meta.get('encoding')}, layer {layer_index} is {encoding}")
+                    shape = tuple(int(v) for v in meta["shape"])
+                    if len(shape) != 2:
+                        raise RuntimeError(f"expert tensor {name!r} is not a matrix")
+                    if shapes.setdefault(proj, shape) != shape:
+                        raise RuntimeError(f"expert tensor {name!r} has unexpected shape {shape!r}")
+                    if meta.get("group_size"):
+                        group = int(meta["group_size"])
+                db, sb = len(views[0][0]), len(views[0][1])
+                if any(len(d) != db or len(sc) != sb for d, sc in views):
+                    raise RuntimeError(f"layer {layer_index} {proj} tensors differ in size")
+                s0 = -(-E * db // 256) * 256  # scales start 256-byte aligned
+                host = stg.take(s0 + E * sb, pinned=dev.type == "cuda")
+                flat = host.numpy()
+                for e, (d, sc) in enumerate(views):
+                    flat[e * db:(e + 1) * db] = np.frombuffer(d, dtype=np.uint8)
+                    if sb:
+                        flat[s0 + e * sb:s0 + (e + 1) * sb] = np.frombuffer(sc, dtype=np.uint8)
+                if dev.type == "cuda":
+                    staged = torch.empty(s0 + E * sb, dtype=torch.uint8, device=dev)
+                    staged.copy_(host, non_blocking=True)
+                    torch.cuda.current_stream(dev).synchronize()  # the buffer is reused for the next projection
+                else:
+                    staged = host
             finally:
-                for v in (data_view, scale_view):
-                    release = getattr(v, "release", None)
-                    if callable(release):
-                        release()
-        data = torch.from_numpy(np.stack(datas))
-        if encoding == "bf16_le":
-            data = data.view(torch.bfloat16)
-        sc = torch.from_numpy(np.stack(scales)).to(device) if scales else None
-        staged[proj] = (data.to(device), sc)
-        shapes[proj] = shape
+                for d, sc in views:
+                    _release(d, sc)
+            rows, cols = shapes[proj]
+            data = staged[:E * db].view({"u1": torch.uint8, "i1": torch.int8, "<u2": torch.bfloat16}[_NP_DTYPE[encoding]])
+            data = data.view(E, rows, -1)
+            sc_t = staged[s0:].view(torch.float32).view(E, -1) if sb else None
+            out[proj] = (data, sc_t)
     inter, hidden = shapes["gate_proj"]
     if shapes["up_proj"] != (inter, hidden) or shapes["down_proj"] != (hidden, inter):
         raise RuntimeError(f"layer {layer_index} projection shapes are inconsistent: {shapes}")
-    return DeviceExperts(
-        encoding,
-        group,
-        num_experts,
-        hidden,
-        inter,
-        staged["gate_proj"][0],
-        staged["gate_proj"][1],
-        staged["up_proj"][0],
-        staged["up_proj"][1],
-        staged["down_proj"][0],
-        staged["down_proj"][1],
-    )
+    return DeviceExperts(encoding, group, E, hidden, inter, out["gate_proj"][0], out["gate_proj"][1], out["up_proj"][0],
+                         out["up_proj"][1], out["down_proj"][0], out["down_proj"][1])
 
 
 class _NativeMoEBackend:
@@ -523,6 +551,10 @@ class _NativeMoEBackend:
         self._cache: dict[tuple[int, str, str], Any] = {}
         self._layer_cache: dict[tuple[int, int, str], DeviceExperts] = {}
         self._lock = threading.Lock()
+        # Raise after every call whose fused launch hit its wait budget (one
+        # host synchronisation per call; off by default: such a launch writes
+        # NaN outputs, and status() checks on demand).
+        self.check_each_call = False
 
     @classmethod
     def build_and_register(cls, *, build_directory: str | Path | None = None, verbose: bool = False):
@@ -560,18 +592,14 @@ class _NativeMoEBackend:
         data_view, scale_view, meta = reader.tensor_views(name)
         try:
             encoding = meta.get("encoding", "q4_group128")
-            dtype_np = {"q4_group128": np.uint8, "q8_group128": np.int8, "bf16_le": np.uint16}[encoding]
-            data = torch.from_numpy(np.frombuffer(data_view, dtype=dtype_np).copy())
+            shape = tuple(int(v) for v in meta["shape"])
+            data = torch.from_numpy(np.frombuffer(data_view, dtype=_NP_DTYPE[encoding]).copy())
             if encoding == "bf16_le":
                 data = data.view(torch.bfloat16)
             scales = (torch.from_numpy(np.frombuffer(scale_view, dtype="<f4").copy()).to(device)
-                      if encoding != "bf16_le" else None)
-            shape = tuple(int(v) for v in meta["shape"])
+                      if ENCODINGS[encoding].grouped else None)
         finally:
-            for v in (data_view, scale_view):
-                release = getattr(v, "release", None)
-                if callable(release):
-                    release()
+            _release(data_view, scale_view)
         if len(shape) != 2:
             raise RuntimeError(f"tensor {name!r} is not a matrix")
         value = (encoding, data.to(device), scales, shape, int(meta.get("group_size") or 128))
@@ -599,23 +627,29 @@ class _NativeMoEBackend:
         return self._linear(input_tensor, pack_handle, name, "q4_group128")
 
     # execution -------------------------------------------------------------
-    def _routed(self, hidden_states, expert_indices, routing_weights, layer_index, pack_handle):
+    def _layer_for_call(self, hidden_states, layer_index, pack_handle):
         import torch
 
         if hidden_states.dtype != torch.bfloat16:
             raise RuntimeError("packed MoE performance backend requires BF16 hidden states")
-        if expert_indices.dtype not in (torch.int32, torch.int64):
-            raise RuntimeError("expert_indices must use int32 or int64")
         with acquire_expert_pack(pack_handle) as reader:
             layer = self._device_layer(pack_handle, layer_index, hidden_states.device, reader)
         if hidden_states.shape[-1] != layer.hidden_size:
             raise RuntimeError(f"hidden size {hidden_states.shape[-1]} does not match the layer's {layer.hidden_size}")
-        flat = hidden_states.reshape(-1, layer.hidden_size)
-        if expert_indices.ndim != 2 or expert_indices.shape[0] != flat.shape[0]:
-            raise RuntimeError("expert_indices must have shape [tokens, top_k]")
         stream = torch.cuda.current_stream(hidden_states.device)
         for t in layer.tensors:
             t.record_stream(stream)
+        return layer
+
+    def _routed(self, hidden_states, expert_indices, routing_weights, layer_index, pack_handle):
+        import torch
+
+        if expert_indices.dtype not in (torch.int32, torch.int64):
+            raise RuntimeError("expert_indices must use int32 or int64")
+        layer = self._layer_for_call(hidden_states, layer_index, pack_handle)
+        flat = hidden_states.reshape(-1, layer.hidden_size)
+        if expert_indices.ndim != 2 or expert_indices.shape[0] != flat.shape[0]:
+            raise RuntimeError("expert_indices must have shape [tokens, top_k]")
         out = self.extension.moe_forward(layer, flat, expert_indices, routing_weights)
         return out.reshape(hidden_states.shape)
 
@@ -627,10 +661,11 @@ class _NativeMoEBackend:
 
     def moe_block(self, hidden_states, router_weight, shared_gate_proj, shared_up_proj, shared_down_proj,
                   shared_expert_gate, top_k, norm_topk_prob, layer_index, pack_handle):
+        """Router + routed experts (+ gated shared expert) of one block;
+        returns (out, router logits, routing weights, expert indices)."""
         import torch
 
-        with acquire_expert_pack(pack_handle) as reader:
-            layer = self._device_layer(pack_handle, layer_index, hidden_states.device, reader)
+        layer = self._layer_for_call(hidden_states, layer_index, pack_handle)
         shared = (shared_gate_proj, shared_up_proj, shared_down_proj, shared_expert_gate)
         if any(t is None for t in shared) and not all(t is None for t in shared):
             raise RuntimeError("shared expert tensors must be given together")
@@ -640,12 +675,17 @@ class _NativeMoEBackend:
         )
         if tuple(dense.router.shape) != (layer.num_experts, layer.hidden_size):
             raise RuntimeError(f"router weight must be [{layer.num_experts}, {layer.hidden_size}]")
-        stream = torch.cuda.current_stream(hidden_states.device)
-        for t in layer.tensors:
-            t.record_stream(stream)
-        return self.extension.moe_layer(layer, dense, hidden_states, int(top_k), bool(norm_topk_prob))
+        result = self.extension.moe_layer(layer, dense, hidden_states, int(top_k), bool(norm_topk_prob))
+        if self.check_each_call:
+            self.extension.status()
+        return result
 
     # bookkeeping -----------------------------------------------------------
+    def status(self) -> None:
+        """Raises if any fused launch since the last check hit its wait
+        budget (its outputs are NaN); synchronises the workspaces' streams."""
+        self.extension.status()
+
     def cache_summary(self) -> dict[str, int]:
         with self._lock:
             tensors = list(self._cache.values())
@@ -668,7 +708,7 @@ class _NativeMoEBackend:
 class PackedQ4NativeBackend(_NativeMoEBackend):
     """All-Q4 backend (ExpertPack or all-Q4 TargetPack layers)."""
 
-    REQUIRED = ("q4_linear", "q4_moe_forward", "q4_moe_prefill")
+    REQUIRED = ("q4_linear", "q4_moe_forward")
     ENCODINGS = frozenset({"q4_group128"})
 
 
@@ -676,7 +716,7 @@ class MixedTargetNativeBackend(_NativeMoEBackend):
     """Mixed Q4 / Q8 / BF16 TargetPack backend; every encoding runs from its
     stored bytes through the same HIP pipeline (no BF16/F32 expansion)."""
 
-    REQUIRED = ("q4_linear", "q4_moe_forward", "q4_moe_prefill", "q8_linear", "q8_moe_forward", "q8_moe_prefill")
+    REQUIRED = ("q4_linear", "q4_moe_forward", "q8_linear", "q8_moe_forward", "bf16_linear")
     ENCODINGS = frozenset({"q4_group128", "q8_group128", "bf16_le"})
 
     def q8_linear(self, input_tensor: Any, pack_handle: int, name: str):
@@ -700,8 +740,10 @@ __all__ = [
     "HipExtension",
     "MixedTargetNativeBackend",
     "PackedQ4NativeBackend",
+    "PinnedStaging",
     "install_mixed_target_backend",
     "install_packed_q4_backend",
+    "layer_expert_count",
     "load_native_extension",
     "native_kernel_source_sha256",
     "observed_native_platform",

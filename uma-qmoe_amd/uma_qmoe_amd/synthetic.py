@@ -22,7 +22,7 @@ import hashlib
 from typing import Any
 
 from .native_backend import EXPERT_NAME, DenseBlock, DeviceExperts
-from .q4 import pack_codes_tensor, quantize_groups_tensor
+from .formats import TargetTensor, encode_projection
 
 SEED = 20260920
 WEIGHT_STD = 0.02
@@ -86,23 +86,6 @@ def hidden_states(shape: MoEShape, tokens: int | None = None, *, seed: int = SEE
 
     t = shape.tokens if tokens is None else tokens
     return normal((t, shape.hidden), seed=_seed(seed, shape.name, tag), std=1.0, device=device).to(torch.bfloat16)
-
-
-def encode_projection(w, encoding: str, group_size: int = 128):
-    """Encode [E, rows, cols] float32 weights per expert -> (data, scales)."""
-    import torch
-
-    e, rows, cols = w.shape
-    if encoding == "bf16_le":
-        return w.to(torch.bfloat16).contiguous(), None
-    flat = w.reshape(e, rows * cols)
-    if encoding == "q4_group128":
-        codes, scales = quantize_groups_tensor(flat, 7, group_size)
-        return pack_codes_tensor(codes).reshape(e, rows, cols // 2).contiguous(), scales.contiguous()
-    if encoding == "q8_group128":
-        codes, scales = quantize_groups_tensor(flat, 127, group_size)
-        return codes.reshape(e, rows, cols).contiguous(), scales.contiguous()
-    raise ValueError(f"unknown encoding {encoding!r}")
 
 
 def build_experts(shape: MoEShape, *, layer: int = 0, seed: int = SEED, device: Any = "cpu",
@@ -212,6 +195,18 @@ class DeviceLayerReader:
 
     def close(self) -> None:
         pass
+
+
+def pack_tensors(layers: dict[int, DeviceExperts]):
+    """(name, TargetTensor) of every routed-expert matrix of staged layers, in
+    the order the pack writers store them (layer, expert, gate/up/down): the
+    bytes of the synthetic layers as a pack would hold them."""
+    reader = DeviceLayerReader(layers)
+    for index in sorted(layers):
+        for name in expert_names(index, layers[index].num_experts):
+            data, scales, meta = reader.tensor_views(name)
+            yield name, TargetTensor(tuple(meta["shape"]), meta["encoding"], bytes(data), bytes(scales),
+                                     meta["group_size"])
 
 
 def expert_names(layer: int, num_experts: int):
