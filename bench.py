@@ -56,10 +56,37 @@ def parse_args():
     return ap.parse_args()
 
 
-def cpu_baseline(shape, seconds: float):
-    """The oracle (reference CPU correctness path restated) on the host cores:
-    transient dequantization every call, FP32 FFN, BF16 index_add_, BF16 shared
-    expert. Bounded: calls repeat until ~``seconds`` of work is done."""
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _time_calls(fn, seconds: float, least: int, most: int):
+    times = []
+    start = time.perf_counter()
+    while time.perf_counter() - start < seconds or len(times) < least:
+        t0 = time.perf_counter_ns()
+        fn()
+        times.append((time.perf_counter_ns() - t0) / 1e3)
+        if len(times) >= most:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline(shape, seconds: float, ext=None):
+    """The oracle (reference CPU correctness path restated) on the host cores,
+    two rows, ~``seconds`` of work in all: (i) as the reference runs it,
+    transient dequantization on every call, FP32 FFN, BF16 index_add_, BF16
+    shared expert; (ii) the same arithmetic on weights dequantized to FP32
+    once (a compute-only CPU bound). With ``ext``, the same token also runs
+    through the HIP block once and the reference_oracle agreement metrics of
+    the two outputs (same routes) and of the two routings are returned."""
     import torch
 
     from oracle import moe as om
@@ -67,6 +94,7 @@ def cpu_baseline(shape, seconds: float):
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    progress(f"cpu baseline: {shape.name} on {cores} host cores")
     layer = syn.build_experts(shape, seed=syn.SEED + 1)
     dense = syn.build_dense(shape, seed=syn.SEED + 1)
     reader = syn.DeviceLayerReader({0: layer})
@@ -76,23 +104,48 @@ def cpu_baseline(shape, seconds: float):
     x = syn.hidden_states(shape, 1)
     for _ in range(2):
         om.qwen_block(x, lay, reader, 0)
-    times = []
-    start = time.perf_counter()
-    while time.perf_counter() - start < seconds or len(times) < 5:
-        t0 = time.perf_counter_ns()
-        om.qwen_block(x, lay, reader, 0)
-        times.append((time.perf_counter_ns() - t0) / 1e3)
-        if len(times) >= 200:
-            break
-    times.sort()
-    med = times[len(times) // 2]
-    return {
+    med, n = _time_calls(lambda: om.qwen_block(x, lay, reader, 0), seconds / 2, 5, 200)
+    weights_of = om.predequantized(reader, 0, shape.num_experts)
+    om.qwen_block(x, lay, reader, 0, weights_of=weights_of)
+    med_pre, n_pre = _time_calls(lambda: om.qwen_block(x, lay, reader, 0, weights_of=weights_of), seconds / 2, 5, 2000)
+    row = {
         "value": round(med, 1),
         "unit": "us/token",
         "cores": cores,
         "kind": "port",
-        "sample": f"median of {len(times)} single-token {shape.name} block calls (oracle, dequantize per call)",
+        "sample": f"median of {n} single-token {shape.name} block calls (oracle, dequantize per call)",
+        "cpu_model": cpu_model(),
+        "predequantized": {"value": round(med_pre, 1), "unit": "us/token",
+                           "sample": f"median of {n_pre} calls with every expert dequantized to FP32 once"},
     }
+    agreement = None
+    if ext is not None:
+        from uma_qmoe_amd.evidence import NORTH_STAR, Q4_LAYER_POLICY, check_policy, numeric_agreement, route_agreement
+
+        dev = torch.device("cuda:0")
+        mv = lambda t: None if t is None else t.to(dev)  # noqa: E731
+        layer_d = syn.DeviceExperts(layer.encoding, layer.group_size, layer.num_experts, layer.hidden_size,
+                                    layer.intermediate_size, *(mv(t) for t in (layer.gate, layer.gate_scales, layer.up,
+                                                                               layer.up_scales, layer.down,
+                                                                               layer.down_scales)))
+        dense_d = syn.DenseBlock(*(mv(t) for t in (dense.router, dense.shared_gate, dense.shared_up, dense.shared_down,
+                                                   dense.shared_expert_gate)))
+        out, _logits, w, idx = ext.moe_layer(layer_d, dense_d, x.to(dev), shape.top_k)
+        torch.cuda.synchronize()
+        ref_same, *_ = om.qwen_block(x, lay, reader, 0, routes=(w.cpu(), idx.cpu()), weights_of=weights_of)
+        _ref, _rl, _rw, ref_idx = om.qwen_block(x, lay, reader, 0, weights_of=weights_of)
+        numeric = numeric_agreement(ref_same, out.cpu(), epsilon=Q4_LAYER_POLICY["relative_error_epsilon"])
+        routes = route_agreement(ref_idx, idx.cpu())
+        agreement = {
+            "scope": f"one {shape.name} token, HIP block vs oracle on the same routes; routes vs the oracle's own",
+            "output": numeric,
+            "routes": routes,
+            "policy": "olmoe_q4_group128_halo3_single_moe_layer_v1 thresholds",
+            "policy_failures": check_policy(numeric, routes, Q4_LAYER_POLICY),
+            "north_star_ok": numeric["rel_l2"] <= NORTH_STAR["max_rel_l2"]
+            and numeric["absolute_error"]["max"] <= NORTH_STAR["max_absolute_error"],
+        }
+    return row, agreement
 
 
 BASELINE_METRIC = "MoE layer \u00b5s/token + achieved HBM GB/s (% peak), Qwen-MoE shape, batch 1 & 32"
@@ -155,12 +208,60 @@ def zipf_routes(torch, syn, shape, x, dense):
     return idx.to(torch.int64).contiguous(), w.contiguous()
 
 
+def progress(msg: str) -> None:
+    """One line per bench phase on stderr (the JSON line alone goes to stdout)."""
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+CV_LIMIT = 0.03
+MIN_SAMPLES = 10
+MIN_TIMED_CALLS = 1300  # >= 100 replays of the 13-instance rotation in all samples together
+
+
+def sample_plan(steps: int) -> int:
+    """Samples of exactly ``steps`` layer calls each: at least MIN_SAMPLES,
+    and enough that all samples together time >= MIN_TIMED_CALLS calls."""
+    return max(MIN_SAMPLES, math.ceil(MIN_TIMED_CALLS / max(1, steps)))
+
+
+def timed_samples(torch, run_calls, steps: int, warmup: int, samples: int, stream=None):
+    """``warmup`` untimed calls, then ``samples`` timings of exactly ``steps``
+    calls each, bracketed by device synchronisations, with HIP events on the
+    stream the kernels run on. ``run_calls(n)`` enqueues n calls. Returns the
+    per-sample milliseconds."""
+    run_calls(warmup)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = []
+    for _ in range(samples):
+        torch.cuda.synchronize()
+        start.record(stream)
+        run_calls(steps)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        out.append(start.elapsed_time(stop))
+    return out
+
+
+def sample_stats(per_call_us):
+    from uma_qmoe_amd.evidence import percentile
+
+    s = sorted(per_call_us)
+    mean = sum(s) / len(s)
+    var = sum((v - mean) ** 2 for v in s) / max(1, len(s) - 1)
+    cv = math.sqrt(var) / mean
+    return {"samples": len(s), "p50_us": round(percentile(s, 0.50), 3), "p95_us": round(percentile(s, 0.95), 3),
+            "p99_us": round(percentile(s, 0.99), 3), "mean_us": round(mean, 3), "cv": round(cv, 5),
+            "cv_limit": CV_LIMIT, "cv_ok": cv <= CV_LIMIT}
+
+
 def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
     """Times one MoE block call on `tokens` tokens: R distinct layer instances
     whose per-call reads together exceed `rotate_bytes` (>= 1 GB, so the 256 MB
-    MALL cannot serve the weights) are captured in one HIP graph, and the
-    graph is replayed between HIP events on torch's current stream (the
-    stream the kernels run on). Returns us per layer call and algorithmic
+    MALL cannot serve the weights) are captured in one HIP graph (plus a graph
+    of the first `steps mod R` calls), and each sample replays exactly `steps`
+    calls between HIP events on torch's current stream (the stream the
+    library launches on). Returns the per-call statistics and algorithmic
     GB/s (each distinct selected expert counted once, plus router and shared
     expert)."""
     dev = torch.device("cuda:0")
@@ -178,13 +279,14 @@ def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
         probe_idx = ext.moe_layer(probe, dense0, x, shape.top_k, workspace=ws)[3]
         probe_bytes = syn.algorithmic_bytes(probe, dense0, int(torch.unique(probe_idx).numel()))
     r_inst = max(2, math.ceil(rotate_bytes / probe_bytes))
+    progress(f"{shape.name} T={tokens}: building {r_inst} layer instances")
     layers = [probe] + [syn.build_experts(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
     denses = [dense0] + [syn.build_dense(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
     outs = [torch.empty((tokens, shape.hidden), dtype=torch.bfloat16, device=dev) for _ in range(r_inst)]
 
-    def run_all():
+    def run_range(n):
         res = []
-        for i in range(r_inst):
+        for i in range(n):
             if routed_only:
                 ext.moe_forward(layers[i], x, fixed[0], fixed[1], out=outs[i], workspace=ws)
                 res.append((outs[i], None, fixed[1], fixed[0]))
@@ -192,12 +294,11 @@ def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
                 res.append(ext.moe_layer(layers[i], denses[i], x, shape.top_k, out=outs[i], workspace=ws))
         return res
 
-    # eager warm-up, then capture the R calls in one graph; a fused launch
-    # whose bounded waits expired (workgroups not all resident) raises here
-    # instead of being timed
-    results = run_all()
+    # eager warm-up; a fused launch that hit its wait budget (workgroups not
+    # all resident) raises here instead of being timed
+    results = run_range(r_inst)
     ext.workspace_status(ws)
-    results = run_all()
+    results = run_range(r_inst)
     torch.cuda.synchronize()
     distinct = [int(torch.unique(res[3]).numel()) for res in results]
     algo_bytes = [syn.algorithmic_bytes(layers[i], None if routed_only else denses[i], distinct[i])
@@ -206,36 +307,39 @@ def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
     flops = sum(layer_flops(shape, tokens, r) for r in valid_routes) / r_inst
     if routed_only:
         flops -= 2.0 * shape.hidden * shape.num_experts * tokens  # the router is not run
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        run_all()
+    graphs = {}
+    for n in {r_inst, steps % r_inst, warmup % r_inst} - {0}:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run_range(n)
+        graphs[n] = g
     torch.cuda.synchronize()
+    progress(f"{shape.name} T={tokens}: graphs captured")
 
-    replays = max(1, math.ceil(steps / r_inst))
-    warm = max(1, math.ceil(warmup / r_inst))
-    for _ in range(warm):
-        graph.replay()
-    torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    samples = []
-    for _ in range(3):
-        torch.cuda.synchronize()
-        start.record()
-        for _ in range(replays):
-            graph.replay()
-        stop.record()
-        torch.cuda.synchronize()
-        samples.append(start.elapsed_time(stop))
-    ms_total = sorted(samples)[1]
+    def run_calls(n):
+        for _ in range(n // r_inst):
+            graphs[r_inst].replay()
+        if n % r_inst:
+            graphs[n % r_inst].replay()
+
+    samples = sample_plan(steps)
+    ms = timed_samples(torch, run_calls, steps, warmup, samples)
     ext.workspace_status(ws)
-    n = replays * r_inst
-    us = ms_total * 1000.0 / n
-    mean_bytes = sum(algo_bytes) / len(algo_bytes)
-    del graph, layers, denses, outs, ws
+    per_call_us = [v * 1000.0 / steps for v in ms]
+    stats = sample_stats(per_call_us)
+    progress(f"{shape.name} T={tokens}: {samples} samples x {steps} calls, p50 {stats['p50_us']} us, "
+             f"cv {stats['cv']}")
+    # the first `steps mod R` instances are timed once more per sample than
+    # the rest: weight the bytes the same way
+    counts = [steps // r_inst + (1 if i < steps % r_inst else 0) for i in range(r_inst)]
+    mean_bytes = sum(c * b for c, b in zip(counts, algo_bytes)) / steps
+    us = stats["p50_us"]
+    del graphs, layers, denses, outs, ws
     torch.cuda.empty_cache()
     return {"us_per_layer": us, "gbps": mean_bytes / (us * 1e-6) / 1e9, "bytes": mean_bytes, "instances": r_inst,
-            "steps": n, "warmup": warm * r_inst, "flops": flops, "tflops": flops / (us * 1e-6) / 1e12,
-            "distinct_experts": sum(distinct) / len(distinct)}
+            "steps": steps, "warmup": warmup, "flops": flops, "tflops": flops / (us * 1e-6) / 1e12,
+            "distinct_experts": sum(distinct) / len(distinct), "stats": stats,
+            "per_call_ms": [v / 1000.0 for v in per_call_us]}
 
 
 def measure_stack(torch, syn, ext, steps_per_rep: int, reps: int):
@@ -251,6 +355,7 @@ def measure_stack(torch, syn, ext, steps_per_rep: int, reps: int):
     from uma_qmoe_amd import _native
 
     dev = torch.device("cuda:0")
+    progress("c3: building 24 layers")
     shapes = [syn.c3_layer_shape(l) for l in range(syn.C3_LAYERS)]
     layers = [syn.build_experts(s, layer=l, device=dev) for l, s in enumerate(shapes)]
     denses = [syn.build_dense(s, layer=l, device=dev) for l, s in enumerate(shapes)]
@@ -300,6 +405,7 @@ def measure_stack(torch, syn, ext, steps_per_rep: int, reps: int):
         if not bool(torch.isfinite(bufs[0].float()).all()):
             raise RuntimeError(f"c3 stack ({mode}) produced non-finite values")
         out[mode] = sorted(samples)[len(samples) // 2]
+        progress(f"c3 {mode}: {out[mode]:.1f} us per token")
         del graph
     ext.set_option(_native.UQM_OPT_FUSED_DECODE, 1)
     del layers, denses, ws
@@ -476,8 +582,12 @@ def main() -> int:
         "mfma_tflops": round(head["tflops"], 2),
         "mfma_frac": round(head["tflops"] / MFMA_PEAK_TFLOPS, 4),
         "distinct_experts": round(head["distinct_experts"], 2),
+        "timing": {**head["stats"], "steps_per_sample": head["steps"]},
         "roofline": roofline,
+        "evidence": evidence_performance(head, shape),
     }
+    if not head["stats"]["cv_ok"]:
+        progress(f"WARNING: sample CV {head['stats']['cv']} exceeds {CV_LIMIT}: timing.cv_ok is false")
     if args.batch32 and tokens == 1 and args.config == "c2":
         b32 = measure(torch, syn, ext, shape, 32, max(32, args.steps // 4), max(8, args.warmup // 4), args.rotate_bytes)
         line["batch32"] = {
@@ -488,11 +598,28 @@ def main() -> int:
             "achieved_gbps": round(b32["gbps"], 1),
             "frac": round(b32["gbps"] / HBM_PEAK_GBPS, 4),
             "distinct_experts": round(b32["distinct_experts"], 2),
+            "timing": {**b32["stats"], "steps_per_sample": b32["steps"]},
         }
     if not args.no_cpu_baseline and tokens == 1:
-        line["cpu_baseline"] = cpu_baseline(shape, args.cpu_seconds)
+        line["cpu_baseline"], line["reference_oracle"] = cpu_baseline(shape, args.cpu_seconds, ext)
+    progress("done")
     print(json.dumps(line), flush=True)
     return 0
+
+
+def evidence_performance(head, shape) -> dict:
+    """The performance block of a packed_q4_kernel_evidence record for this
+    measurement: per-call milliseconds of every sample, median, nearest-rank
+    p95, and one layer's compressed expert bytes (nothing dequantized)."""
+    from uma_qmoe_amd.evidence import timing
+
+    t = timing(head["per_call_ms"])
+    per_expert = {"q4_group128": 0.5 + 4 / 128, "q8_group128": 1 + 4 / 128, "bf16_le": 2}[shape.encoding]
+    expert_bytes = int(shape.num_experts * 3 * shape.hidden * shape.intermediate * per_expert)
+    return {"scope": "single_moe_layer_microbenchmark", "samples_milliseconds": [round(v, 6) for v in t["samples_milliseconds"]],
+            "median_milliseconds": round(t["median_milliseconds"], 6), "p95_milliseconds": round(t["p95_milliseconds"], 6),
+            "compressed_cache_tensor_count": 3 * shape.num_experts, "compressed_cache_bytes": expert_bytes,
+            "dequantized_weight_cache_bytes": 0, "formal_tps_claim": False}
 
 
 if __name__ == "__main__":

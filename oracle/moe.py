@@ -65,6 +65,25 @@ def _fused_gate_up(selected: torch.Tensor, gate_up: torch.Tensor) -> torch.Tenso
     return intermediate
 
 
+def decoded_expert(reader: Any, layer_index: int, e: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """FP32 ([gate; up], down) of one expert, dequantized from the reader
+    (src/uma_qmoe/custom_op.py:475-490, _combine_gate_up_arrays :35-40)."""
+    gate = read_tensor(reader, expert_name(layer_index, e, "gate_proj"))
+    up = read_tensor(reader, expert_name(layer_index, e, "up_proj"))
+    down = read_tensor(reader, expert_name(layer_index, e, "down_proj"))
+    if gate.shape != up.shape:
+        raise RuntimeError("Gate and Up projection shapes must match")
+    return torch.from_numpy(np.concatenate((gate, up), axis=0)), torch.from_numpy(np.ascontiguousarray(down))
+
+
+def predequantized(reader: Any, layer_index: int, num_experts: int):
+    """All experts of a layer dequantized once; a ``weights_of`` for
+    streaming_reference that then does only the FP32 arithmetic (the
+    compute-only CPU bound: the reference dequantizes on every call)."""
+    table = {e: decoded_expert(reader, layer_index, e) for e in range(num_experts)}
+    return table.__getitem__
+
+
 def streaming_reference(
     hidden_states: torch.Tensor,
     expert_indices: torch.Tensor,
@@ -73,11 +92,16 @@ def streaming_reference(
     reader: Any,
     *,
     num_experts: int,
+    weights_of=None,
 ) -> torch.Tensor:
     """CPU correctness branch of the operator, generic in E and k.
 
-    src/uma_qmoe/custom_op.py:465-506 (Qwen) / :307-340 (OLMoE).
+    src/uma_qmoe/custom_op.py:465-506 (Qwen) / :307-340 (OLMoE). Experts are
+    dequantized per call from ``reader`` unless ``weights_of(e)`` supplies
+    them.
     """
+    if weights_of is None:
+        weights_of = lambda e: decoded_expert(reader, layer_index, e)  # noqa: E731
     flattened = hidden_states.reshape(-1, hidden_states.shape[-1])
     final = torch.zeros_like(flattened)
     if flattened.shape[0] == 0:
@@ -88,13 +112,7 @@ def streaming_reference(
     for entry in hit:
         e = int(entry[0].item())
         slots, rows = torch.where(mask[e])
-        gate = read_tensor(reader, expert_name(layer_index, e, "gate_proj"))
-        up = read_tensor(reader, expert_name(layer_index, e, "up_proj"))
-        down = read_tensor(reader, expert_name(layer_index, e, "down_proj"))
-        if gate.shape != up.shape:
-            raise RuntimeError("Gate and Up projection shapes must match")
-        gate_up = torch.from_numpy(np.concatenate((gate, up), axis=0))
-        down_t = torch.from_numpy(np.ascontiguousarray(down))
+        gate_up, down_t = weights_of(e)
         selected = flattened.index_select(0, rows).to(torch.float32)
         intermediate = _fused_gate_up(selected, gate_up)
         expert_output = F.linear(intermediate, down_t)
@@ -195,7 +213,7 @@ def shared_expert(hidden, gate_w, up_w, down_w, shared_gate_w):
     return torch.sigmoid(F.linear(hidden, shared_gate_w)) * y
 
 
-def qwen_block(hidden, layer, reader, layer_index: int, *, routes=None):
+def qwen_block(hidden, layer, reader, layer_index: int, *, routes=None, weights_of=None):
     """QuantizedQwenMoEBlock.forward, src/uma_qmoe/qwen_compressed_loader.py:67-86.
 
     ``layer`` holds the dense BF16 tensors: router [E,H], shared_gate/up [Is,H],
@@ -207,7 +225,8 @@ def qwen_block(hidden, layer, reader, layer_index: int, *, routes=None):
     logits, weights, indices = router(flat, layer["router"], layer["top_k"], layer.get("norm_topk_prob", False))
     if routes is not None:
         weights, indices = routes
-    out = streaming_reference(flat, indices, weights, layer_index, reader, num_experts=layer["num_experts"])
+    out = streaming_reference(flat, indices, weights, layer_index, reader, num_experts=layer["num_experts"],
+                              weights_of=weights_of)
     if layer.get("shared_gate") is not None:
         sh = shared_expert(flat, layer["shared_gate"], layer["shared_up"], layer["shared_down"], layer["shared_expert_gate"])
         out = out.add_(sh)

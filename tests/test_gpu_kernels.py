@@ -71,6 +71,21 @@ def assert_bf16_rounded(got: torch.Tensor, ref: torch.Tensor, what: str, rel=4e-
     assert worst <= 0.0, f"{what}: an element exceeds one bf16 rounding + {slack}"
 
 
+def assert_weights_follow_logits(logits, weights, indices, norm=False, what="routing weights"):
+    """weights == bf16(softmax_f32(logits)[indices]) (renormalised over the k
+    selected when ``norm``), to one bf16 ulp; indices bit-exact given the logits."""
+    lc, wc, ic = logits.cpu(), weights.cpu(), indices.cpu()
+    assert torch.equal(ic, om.topk_ordered(lc, ic.shape[-1])), f"{what}: indices"
+    p = torch.softmax(lc.float(), dim=-1).gather(-1, ic)
+    if norm:
+        p = p / p.sum(-1, keepdim=True)
+    ref = p.to(torch.bfloat16).view(torch.int16).int()
+    got = wc.to(torch.bfloat16).view(torch.int16).int()
+    ulps = int((ref - got).abs().max())
+    print(f"  {what}: max bf16 ulp difference {ulps}", flush=True)
+    assert ulps <= 1, f"{what}: weights differ from softmax(logits) by {ulps} ulp"
+
+
 # ------------------------------------------------------------------ linear --
 @pytest.mark.parametrize("encoding", ["q4_group128", "q8_group128", "bf16_le"])
 @pytest.mark.parametrize("rows,n,k", [(1, 64, 2048), (3, 96, 1408), (7, 40, 768), (4, 256, 5632)])
@@ -307,7 +322,7 @@ def test_block_topk_permute_fusion_boundary(hip_ext, t):
     out, logits, weights, indices = hip_ext.moe_layer(layer, dense, x.to(DEV), shape.top_k)
     out = out.clone()
     logits_c, weights_c, indices_c = logits.cpu(), weights.cpu(), indices.cpu()
-    assert torch.equal(indices_c, om.topk_ordered(logits_c, shape.top_k))
+    assert_weights_follow_logits(logits_c, weights_c, indices_c, False, f"fusion boundary t={t}")
     dense_c = DenseBlock(*(None if v is None else v.cpu() for v in (
         dense.router, dense.shared_gate, dense.shared_up, dense.shared_down, dense.shared_expert_gate)))
     lay = {"router": dense_c.router, "top_k": shape.top_k, "num_experts": shape.num_experts,

@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from oracle import moe as om
+from test_gpu_kernels import assert_weights_follow_logits
 from uma_qmoe_amd import _native
 from uma_qmoe_amd import synthetic as syn
 from uma_qmoe_amd.native_backend import DenseBlock, DeviceExperts
@@ -152,7 +153,7 @@ def test_qwen_block_batched_decode(mfma_on, t):
     x = syn.hidden_states(shape, t, seed=40 + t)
     (out, logits, weights, indices), (out_g, *_rest) = both_paths(
         ext, lambda: ext.moe_layer(layer, dense, x.to(DEV), shape.top_k))
-    assert torch.equal(indices.cpu(), om.topk_ordered(logits.cpu(), shape.top_k))
+    assert_weights_follow_logits(logits, weights, indices, False, f"c2 block t={t}")
     ref, *_ = om.qwen_block(x, layout_of(shape, dense_cpu(dense)), syn.DeviceLayerReader({0: layer}), 0,
                             routes=(weights.cpu(), indices.cpu()))
     close(out, ref, f"c2 block t={t}")
@@ -209,7 +210,7 @@ def test_c4_prefill_512_tokens(mfma_on):
     x = syn.hidden_states(shape, 512, seed=4)
     (out, logits, weights, indices), (out_g, *_rest) = both_paths(
         ext, lambda: ext.moe_layer(layer, dense, x.to(DEV), shape.top_k))
-    assert torch.equal(indices.cpu(), om.topk_ordered(logits.cpu(), shape.top_k))
+    assert_weights_follow_logits(logits, weights, indices, False, "c4 (512 tokens)")
     close(out, out_g, "c4 mfma vs gemv (512 tokens)", rel=5e-3, mx=1e-2)
     pick = torch.randperm(512, generator=torch.Generator().manual_seed(9))[:16].sort().values
     ref, *_ = om.qwen_block(x[pick], layout_of(shape, dense_cpu(dense)), syn.DeviceLayerReader({0: layer}), 0,

@@ -250,6 +250,10 @@ def write_expert_pack(destination: str | Path, tensors: Iterable[tuple[str, Any]
 
     def items():
         for name, values in tensors:
+            if isinstance(values, TargetTensor):
+                if values.encoding != Q4.name:
+                    raise ContractError(f"ExpertPack tensor {name!r} is {values.encoding}, not Q4")
+                values = Q4Tensor(values.shape, values.group_size or GROUP_SIZE, values.data, values.scales)
             if isinstance(values, Q4Tensor):
                 if values.group_size != group_size:
                     raise ContractError("pre-encoded Q4 tensor group size differs from the pack's")
