@@ -35,7 +35,7 @@ from uma_qmoe_amd.custom_op import (
     register_target_pack,
     unregister_expert_pack,
 )
-from uma_qmoe_amd.formats import decode_target_tensor, encode_target_tensor
+from uma_qmoe_amd.formats import decode_target_tensor
 from uma_qmoe_amd.native_backend import install_mixed_target_backend, install_packed_q4_backend
 from uma_qmoe_amd.packfile import ExpertPackReader, TargetPackReader, memory_pack, write_expert_pack, write_target_pack
 
@@ -195,10 +195,6 @@ def test_c3_mixed_layers_from_memory_pack():
     layers = {l: syn.build_experts(syn.c3_layer_shape(l), layer=l, device=DEV) for l in (0, 16)}
     denses = {l: syn.build_dense(syn.c3_layer_shape(l), layer=l, device=DEV) for l in (0, 16)}
     tensors = dict(syn.pack_tensors(layers))
-    # one tensor re-encoded from its float values with the product codec: same bytes
-    name = "model.layers.16.mlp.experts.3.down_proj.weight"
-    again = encode_target_tensor(decode_target_tensor(tensors[name]), "q8_group128")
-    assert again == tensors[name]
     policy = {i: ("bf16_le" if i < 16 else "q8_group128") for i in range(24)}
     pack = memory_pack(tensors, policy, num_experts=60)
     handle = register_target_pack(pack)
