@@ -13,7 +13,7 @@ moe    torch-CPU restatement of the operator's correctness path, the
 
 Pinning (what checks each function; see tests/test_oracle_*.py):
   codec       reference known-answer vectors (tests/unit/test_q4.py:19-67,
-              tests/unit/test_bf16.py:111-129) + closed forms + brute force
+              tests/unit/test_bf16.py:44-63) + closed forms + brute force
   router      brute-force sort on tiny inputs, forced ties, Transformers'
               Qwen2MoeTopKRouter on tie-free inputs
   experts     Transformers' Qwen2MoeExperts / Qwen2MoeSparseMoeBlock run in fp32

@@ -16,7 +16,7 @@
  *   Q8   src/uma_qmoe/target_pack.py:92-112   scale = absmax/127, clip +-127
  *        src/uma_qmoe/target_pack.py:164-175  dequantize
  *   BF16 src/uma_qmoe/target_pack.py:78-89    RNE (w + 0x7FFF + lsb) >> 16
- *        src/uma_qmoe/bf16.py (NaN handling pinned by tests/unit/test_bf16.py:111-129)
+ *        src/uma_qmoe/bf16.py (NaN handling pinned by tests/unit/test_bf16.py:44-63)
  *
  * numpy semantics reproduced exactly: float32 division by a Python int is a
  * float32 division (NEP 50), np.rint is round-half-to-even, which is rintf()

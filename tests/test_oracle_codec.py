@@ -4,7 +4,7 @@ against it bit for bit.
 Known-answer vectors come from the reference's own tests:
   tests/unit/test_q4.py:19-67     nibble order, 129-element layout, -8 and
                                   tail rejection, zero groups, bad scales
-  tests/unit/test_bf16.py:111-129 f32 -> bf16 round-to-nearest-even words
+  tests/unit/test_bf16.py:44-63 f32 -> bf16 round-to-nearest-even words
 What those leave open (the choice of code for every value) is pinned by
 brute force: each code must be the nearest grid point, ties to even.
 """
@@ -64,7 +64,7 @@ def test_q4_rejects_invalid_scales(scale):
 
 
 def test_bf16_round_to_nearest_even_known_answers():
-    # tests/unit/test_bf16.py:111-129
+    # tests/unit/test_bf16.py:44-63
     words = [0x3F808000, 0x3F818000, 0x7F800000, 0xFF800000, 0x7F800001, 0xFF800001]
     f = np.array(words, dtype=np.uint32).view(np.float32)
     assert oc.f32_to_bf16_bits(f).tolist() == [0x3F80, 0x3F82, 0x7F80, 0xFF80, 0x7FC0, 0xFFC0]

@@ -1,0 +1,228 @@
+// Per-phase timeline of the single-token fused MoE kernel (uqm_fused.hip).
+//
+// The kernel's trace hooks are defined here to store, for every wave, the
+// wall clock (s_memrealtime) at each phase boundary; the kernel source is
+// then included unchanged. The program builds `instances` layers of one
+// configuration with arbitrary weight bytes (the timing does not depend on
+// the values; every nibble and bf16 pattern decodes to a finite number),
+// times `reps` rotations over them with HIP events, then traces one more
+// rotation and prints, per phase boundary, when the waves reached it
+// (microseconds after the first wave of the launch started), averaged over
+// the traced launches. Usage:
+//   fused_timeline [c2|c1] [instances=13] [reps=40]
+// Phase boundaries (streaming waves unless noted):
+//   0 entry
+//   1 control wave: router rows published
+//   2 control wave: logits of all router rows seen (poll done)
+//   3 control wave: routes and weights in LDS
+//   4 phase A (shared gate/up products) done
+//   5 routes read after the workgroup barrier
+//   6 phase B (routed gate/up products) done
+//   7 phase-C loads issued, shared products staged
+//   8 routed products staged, fragments built
+//   9 output rows written
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <vector>
+
+__device__ unsigned long long* g_trace;  // [launch wave][16] wall-clock stamps, NULL: off
+
+#define UQM_FUSED_TRACE_INIT unsigned long long* const trace_base_ = g_trace;
+#define UQM_FUSED_TRACE(p)                                                                     \
+  do {                                                                                         \
+    if ((threadIdx.x & 63) == 0 && trace_base_ != nullptr)                                     \
+      trace_base_[static_cast<size_t>(gw) * 16 + (p)] = __builtin_amdgcn_s_memrealtime();      \
+  } while (0)
+
+#include "../uqm_fused.hip"
+
+#define CHECK(x)                                                                   \
+  do {                                                                             \
+    hipError_t e_ = (x);                                                           \
+    if (e_ != hipSuccess) {                                                        \
+      fprintf(stderr, "HIP error %s at line %d\n", hipGetErrorString(e_), __LINE__); \
+      exit(1);                                                                     \
+    }                                                                              \
+  } while (0)
+
+namespace {
+
+__global__ void fill_words(uint32_t* p, size_t n, uint32_t seed, uint32_t mask, uint32_t bias) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    uint32_t h = static_cast<uint32_t>(i) * 2654435761u ^ seed;
+    h ^= h >> 13;
+    h *= 0x5bd1e995u;
+    h ^= h >> 15;
+    p[i] = (h & mask) | bias;
+  }
+}
+
+// Small finite bf16 values (magnitudes in [2^-5, 2^-1)), two per word.
+void fill_bf16(void* p, size_t elems, uint32_t seed) {
+  hipLaunchKernelGGL(fill_words, dim3(1024), dim3(256), 0, 0, static_cast<uint32_t*>(p), elems / 2, seed,
+                     0x81FF81FFu, 0x3D003D00u);
+}
+void fill_bytes(void* p, size_t bytes, uint32_t seed) {
+  hipLaunchKernelGGL(fill_words, dim3(1024), dim3(256), 0, 0, static_cast<uint32_t*>(p), bytes / 4, seed,
+                     0xFFFFFFFFu, 0u);
+}
+void fill_scales(float* p, size_t n) {  // 2^-8
+  hipLaunchKernelGGL(fill_words, dim3(256), dim3(256), 0, 0, reinterpret_cast<uint32_t*>(p), n, 0u, 0u, 0x3B800000u);
+}
+
+template <typename T>
+T* device_alloc(size_t n) {
+  void* p = nullptr;
+  CHECK(hipMalloc(&p, n * sizeof(T)));
+  return static_cast<T*>(p);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const char* config = argc > 1 ? argv[1] : "c2";
+  const int R = argc > 2 ? atoi(argv[2]) : 13;
+  const int reps = argc > 3 ? atoi(argv[3]) : 40;
+  const bool c1 = strcmp(config, "c1") == 0;
+  const int64_t H = 2048, I = c1 ? 1024 : 1408, Is = c1 ? 0 : 5632;
+  const int E = c1 ? 64 : 60, k = c1 ? 8 : 4, G = 128;
+  if (R < 1 || reps < 1) {
+    fprintf(stderr, "usage: fused_timeline [c2|c1] [instances>=1] [reps>=1]\n");
+    return 2;
+  }
+  const size_t ws_bytes = 1 << 20;
+  char* ws = device_alloc<char>(ws_bytes);
+  CHECK(hipMemset(ws, 0, ws_bytes));
+  uint16_t* x = device_alloc<uint16_t>(H);
+  uint16_t* out = device_alloc<uint16_t>(H);
+  fill_bf16(x, H, 7);
+  std::vector<uqm::FusedArgs> inst(R);
+  size_t bytes_per_call = 0;
+  for (int r = 0; r < R; ++r) {
+    uqm::FusedArgs& a = inst[r];
+    memset(&a, 0, sizeof(a));
+    const size_t routed = static_cast<size_t>(E) * I * H / 2, scales = static_cast<size_t>(E) * I * H / G;
+    uint16_t* router = device_alloc<uint16_t>(E * H);
+    fill_bf16(router, E * H, 100 + r);
+    uint8_t* eg = device_alloc<uint8_t>(routed);
+    uint8_t* eu = device_alloc<uint8_t>(routed);
+    uint8_t* ed = device_alloc<uint8_t>(routed);
+    float* sc = device_alloc<float>(3 * scales);
+    fill_bytes(eg, routed, 600 + r);
+    fill_bytes(eu, routed, 700 + r);
+    fill_bytes(ed, routed, 800 + r);
+    fill_scales(sc, 3 * scales);
+    a.router = reinterpret_cast<const uint8_t*>(router);
+    if (Is > 0) {
+      uint16_t* seg = device_alloc<uint16_t>(H);
+      uint16_t* sg = device_alloc<uint16_t>(Is * H);
+      uint16_t* su = device_alloc<uint16_t>(Is * H);
+      uint16_t* sd = device_alloc<uint16_t>(Is * H);
+      fill_bf16(seg, H, 200 + r);
+      fill_bf16(sg, Is * H, 300 + r);
+      fill_bf16(su, Is * H, 400 + r);
+      fill_bf16(sd, Is * H, 500 + r);
+      a.shared_expert_gate = reinterpret_cast<const uint8_t*>(seg);
+      a.sg_w = reinterpret_cast<const uint8_t*>(sg);
+      a.su_w = reinterpret_cast<const uint8_t*>(su);
+      a.sd_w = reinterpret_cast<const uint8_t*>(sd);
+    }
+    a.eg = eg;
+    a.eu = eu;
+    a.ed = ed;
+    a.egs = sc;
+    a.eus = sc + scales;
+    a.eds = sc + 2 * scales;
+    a.x = x;
+    a.out = out;
+    a.H = H;
+    a.I = I;
+    a.Is = Is;
+    a.E = E;
+    a.k = k;
+    a.group = G;
+    a.wait_ticks = 200000;  // 2 ms at 100 MHz
+    a.sync = reinterpret_cast<uint32_t*>(ws);
+    a.hs = reinterpret_cast<uint32_t*>(ws + 8192);
+    a.hr = reinterpret_cast<uint32_t*>(ws + 8192 + 4 * 8192);
+    a.lgt = reinterpret_cast<uint64_t*>(ws + 8192 + 8 * 8192);
+    bytes_per_call = static_cast<size_t>(k) * (3 * (I * H / 2) + 3 * (I * H / G) * 4) + static_cast<size_t>(E) * H * 2 +
+                     (Is > 0 ? 3 * Is * H * 2 + H * 2 : 0);
+  }
+  CHECK(hipDeviceSynchronize());
+  int dev = 0, cus = 0, khz = 0;
+  CHECK(hipGetDevice(&dev));
+  CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+  const int waves = cus * 9;
+
+  // timed rotations, tracing off
+  hipEvent_t e0, e1;
+  CHECK(hipEventCreate(&e0));
+  CHECK(hipEventCreate(&e1));
+  for (int w = 0; w < 3; ++w)
+    for (int r = 0; r < R; ++r) CHECK(uqm::launch_moe_decode_fused(uqm::kQ4, inst[r], 0));
+  CHECK(hipEventRecord(e0, 0));
+  for (int i = 0; i < reps; ++i)
+    for (int r = 0; r < R; ++r) CHECK(uqm::launch_moe_decode_fused(uqm::kQ4, inst[r], 0));
+  CHECK(hipEventRecord(e1, 0));
+  CHECK(hipEventSynchronize(e1));
+  float ms = 0.f;
+  CHECK(hipEventElapsedTime(&ms, e0, e1));
+  const double us_call = 1000.0 * ms / (reps * R);
+
+  // one traced rotation: launch r writes its stamps to trace + r * waves * 16
+  const size_t per_launch = static_cast<size_t>(waves) * 16;
+  unsigned long long* trace = device_alloc<unsigned long long>(per_launch * R);
+  CHECK(hipMemset(trace, 0, per_launch * R * sizeof(unsigned long long)));
+  for (int r = 0; r < R; ++r) {
+    unsigned long long* p = trace + r * per_launch;
+    CHECK(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &p, sizeof(p)));
+    CHECK(uqm::launch_moe_decode_fused(uqm::kQ4, inst[r], 0));
+    CHECK(hipDeviceSynchronize());
+  }
+  unsigned long long* none = nullptr;
+  CHECK(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &none, sizeof(none)));
+  std::vector<unsigned long long> host(per_launch * R);
+  CHECK(hipMemcpy(host.data(), trace, host.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost));
+  uint32_t err = 0;
+  CHECK(hipMemcpy(&err, ws + 4 * uqm::kSyncError, 4, hipMemcpyDeviceToHost));
+
+  // per point and wave kind: average over launches of the min / median / max
+  // over waves of (stamp - first entry stamp of the launch)
+  const double tick_us = 1000.0 / khz;
+  printf("{\"config\": \"%s\", \"instances\": %d, \"reps\": %d, \"cus\": %d, \"us_per_call\": %.3f, "
+         "\"algorithmic_bytes_per_call\": %zu, \"tb_per_s\": %.3f, \"error_word\": %u, \"clock_khz\": %d}\n",
+         config, R, reps, cus, us_call, bytes_per_call, bytes_per_call / us_call / 1e6, err, khz);
+  printf("point  waves      min_us  median_us   max_us\n");
+  for (int p = 0; p < 10; ++p) {
+    for (int kind = 0; kind < 2; ++kind) {  // 0 streaming waves, 1 control waves
+      double acc[3] = {0, 0, 0};
+      int used = 0;
+      for (int r = 0; r < R; ++r) {
+        const unsigned long long* t = host.data() + r * per_launch;
+        unsigned long long t0 = ~0ull;
+        for (int w = 0; w < waves; ++w)
+          if (t[w * 16] != 0) t0 = std::min(t0, t[w * 16]);
+        std::vector<double> v;
+        for (int w = 0; w < waves; ++w)
+          if ((w % 9 == 8) == (kind == 1) && t[w * 16 + p] != 0) v.push_back((t[w * 16 + p] - t0) * tick_us);
+        if (v.empty()) continue;
+        std::sort(v.begin(), v.end());
+        acc[0] += v.front();
+        acc[1] += v[v.size() / 2];
+        acc[2] += v.back();
+        ++used;
+      }
+      if (used == 0) continue;
+      printf("%5d  %-9s %8.2f  %9.2f  %7.2f\n", p, kind ? "control" : "streaming", acc[0] / used, acc[1] / used,
+             acc[2] / used);
+    }
+  }
+  return err == 0 ? 0 : 3;
+}

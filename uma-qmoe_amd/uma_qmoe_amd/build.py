@@ -1,7 +1,9 @@
 """Builds libuma_qmoe_hip.so for gfx950 with hipcc (in-tree, no JIT cache).
 
 Each ``csrc/*.hip`` translation unit is compiled in parallel to an object
-under ``_build/`` and linked into ``uma-qmoe_amd/lib/libuma_qmoe_hip.so``.
+under ``_build/`` and linked into ``uma-qmoe_amd/lib/libuma_qmoe_hip.so``;
+``csrc/timeline/fused_timeline.hip`` becomes the program
+``uma-qmoe_amd/lib/fused_timeline``.
 Run as ``python -m uma_qmoe_amd.build`` with ``uma-qmoe_amd`` on sys.path.
 """
 
@@ -49,16 +51,35 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+TIMELINE_SRC = CSRC / "timeline" / "fused_timeline.hip"
+TIMELINE_PATH = LIB_DIR / "fused_timeline"
+
+
+def _compile_timeline() -> Path:
+    """The per-phase timeline program of the single-token fused kernel
+    (csrc/timeline/fused_timeline.hip includes csrc/uqm_fused.hip)."""
+    tmp = TIMELINE_PATH.with_suffix(".tmp")
+    cmd = [HIPCC, *[f for f in COMMON_FLAGS if f != "-fPIC"], str(TIMELINE_SRC), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {TIMELINE_SRC.name}:\n{proc.stderr}")
+    os.replace(tmp, TIMELINE_PATH)
+    return TIMELINE_PATH
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile every HIP source and link the shared library. Always rebuilds."""
+    """Compile every HIP source, link the shared library and build the
+    timeline program. Always rebuilds."""
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    jobs = min(len(srcs) + 1, max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
+        timeline = pool.submit(_compile_timeline)
         objs = list(pool.map(_compile, srcs))
+        timeline.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)

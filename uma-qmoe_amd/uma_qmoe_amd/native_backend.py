@@ -485,7 +485,10 @@ def stage_experts(reader: Any, layer_index: int, device: Any, num_experts: int |
     dev = torch.device(device)
     out: dict[str, tuple[Any, Any]] = {}
     shapes: dict[str, tuple[int, int]] = {}
-    group = 128
+    # an ExpertPack names its group size in the header, a TargetPack per tensor
+    header = getattr(reader, "header", None)
+    quant = header.get("quantization") if isinstance(header, dict) else None
+    group = int(quant.get("group_size", 128)) if isinstance(quant, dict) else 128
     with stg.lock:
         for proj in PROJECTIONS:
             views = []
