@@ -198,6 +198,25 @@ int uqm_set_option(int option, int64_t value);
  * clean. No counterpart in the reference. */
 int uqm_workspace_status(void* workspace, size_t workspace_bytes, void* stream);
 
+/* Scratch bytes uqm_moe_layer_noalloc holds per device (16 MiB: c2 shapes up
+ * to ~80 tokens; uqm_moe_workspace_bytes gives what a call needs). */
+#define UQM_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+
+/* uqm_moe_layer without a workspace argument and without any allocation: the
+ * temporaries live in a library-owned device array of
+ * UQM_NOALLOC_SCRATCH_BYTES per device, held until the process ends. No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Calls needing more than the array hold
+ * fail with UQM_ERR_WORKSPACE. The first call on a device zero-fills the
+ * array on `stream` and must not be under graph capture. Every call on one
+ * GPU shares that GPU's array (it keeps the last call's contents), so calls
+ * that overlap in time on one GPU race; calls in order on one stream are
+ * safe. The shared expert runs on `stream` (no side stream). Otherwise as
+ * uqm_moe_layer, with the same kernels and results. */
+int uqm_moe_layer_noalloc(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, void* output,
+                          void* logits, void* routing_weights, int64_t* expert_indices, void* stream);
+
 /* RMSNorm (Transformers Qwen2MoeRMSNorm, modeling_qwen2_moe.py:65-70): bf16 in/out,
  * FP32 variance; weight bf16 [H] or NULL for ones. Used by the 24-layer stack driver. */
 int uqm_rmsnorm(const void* input, int64_t rows, int64_t hidden_size, const void* weight, float eps,

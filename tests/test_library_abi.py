@@ -69,3 +69,22 @@ def test_set_option_is_host_only_and_validates():
     assert lib.uqm_set_option(99, 1) != 0
     assert b"unknown option" in lib.uqm_last_error()
     assert lib.uqm_set_option(_native.UQM_OPT_MFMA_MIN_TOKENS, -1) != 0
+
+
+def test_noalloc_limit_is_checked_on_the_host():
+    """UQM_NOALLOC_SCRATCH_BYTES matches the Python constant, and a call whose
+    workspace would exceed it is refused before anything touches a device."""
+    import ctypes
+
+    text = HEADER.read_text()
+    m = re.search(r"#define\s+UQM_NOALLOC_SCRATCH_BYTES\s+\(\(size_t\)(\d+)\s*<<\s*(\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == _native.NOALLOC_SCRATCH_BYTES
+    lib = _native.library()
+    experts = _native.ExpertWeights(_native.UQM_Q4, 128, 60, 2048, 1408, 16, 16, 16, 16, 16, 16)
+    layer = _native.LayerWeights(experts, 16, 4, 0, 1, 5632, 16, 16, 16, 16)
+    need = lib.uqm_moe_workspace_bytes(1000, 2048, 1408, 5632, 60, 4)
+    assert need > _native.NOALLOC_SCRATCH_BYTES
+    rc = lib.uqm_moe_layer_noalloc(ctypes.byref(layer), 16, 1000, 16, None, None, None, None)
+    assert rc == 4  # UQM_ERR_WORKSPACE
+    assert b"uqm_moe_layer_noalloc" in lib.uqm_last_error() and b"workspace" in lib.uqm_last_error()
+    assert lib.uqm_moe_layer_noalloc(None, 16, 1, 16, None, None, None, None) == 1

@@ -674,7 +674,7 @@ struct InputNorm {
 
 int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, InputNorm norm, void* output,
                    void* logits, void* routing_weights, int64_t* expert_indices, void* workspace,
-                   size_t workspace_bytes, void* stream) {
+                   size_t workspace_bytes, void* stream, bool allow_side_stream = true) {
   using namespace uqm;
   int rc = check_device();
   if (rc) return rc;
@@ -781,7 +781,7 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
     }
   } join_on_exit{s};
   if (layer->has_shared) {
-    if (g_opt_overlap_shared.load(std::memory_order_relaxed) != 0) {
+    if (allow_side_stream && g_opt_overlap_shared.load(std::memory_order_relaxed) != 0) {
       side_lock = std::unique_lock<std::mutex>(g_side_mu);
       side = side_stream(s);
     }
@@ -870,6 +870,31 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
 }
 
 }  // namespace
+
+}  // extern "C"
+
+namespace uqm {
+
+int api_fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int moe_layer_on_workspace(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, void* output,
+                           void* logits, void* routing_weights, int64_t* expert_indices, void* workspace,
+                           size_t workspace_bytes, bool side_stream, void* stream) {
+  return moe_layer_impl(layer, hidden, tokens, InputNorm{false, nullptr, 0.f}, output, logits, routing_weights,
+                        expert_indices, workspace, workspace_bytes, stream, side_stream);
+}
+
+}  // namespace uqm
+
+extern "C" {
 
 int uqm_moe_layer(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, void* output, void* logits,
                   void* routing_weights, int64_t* expert_indices, void* workspace, size_t workspace_bytes,

@@ -8,6 +8,8 @@
 
 #include "uqm_device.h"
 
+struct uqm_layer_weights;  // include/uma_qmoe_hip.h
+
 namespace uqm {
 
 enum GemvMode : int { kModeSilu = 0, kModeF32 = 1, kModeBF16 = 2 };
@@ -170,5 +172,14 @@ hipError_t launch_moe_decode_fused(int enc, const FusedArgs& a, hipStream_t stre
 
 hipError_t launch_rmsnorm(const uint16_t* x, int64_t rows, int64_t H, const uint16_t* weight, float eps,
                           uint16_t* out, hipStream_t stream);
+
+// Entry-point plumbing shared by the translation units that export C-ABI
+// functions (uqm_api.hip): sets the thread's uqm_last_error message and
+// returns `code`; runs uqm_moe_layer on a given workspace, with or without
+// the shared-expert side stream.
+int api_fail(int code, const char* fmt, ...);
+int moe_layer_on_workspace(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, void* output,
+                           void* logits, void* routing_weights, int64_t* expert_indices, void* workspace,
+                           size_t workspace_bytes, bool side_stream, void* stream);
 
 }  // namespace uqm

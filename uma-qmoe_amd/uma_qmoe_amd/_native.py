@@ -21,6 +21,7 @@ UQM_BF16 = 2
 
 UQM_OPT_FUSED_DECODE = 1
 UQM_OPT_MFMA_MIN_TOKENS = 3
+NOALLOC_SCRATCH_BYTES = 16 << 20  # UQM_NOALLOC_SCRATCH_BYTES
 UQM_OPT_OVERLAP_SHARED = 4
 
 ENCODING_IDS = {"q4_group128": UQM_Q4, "q8_group128": UQM_Q8, "bf16_le": UQM_BF16}
@@ -91,6 +92,10 @@ SIGNATURES = {
     "uqm_moe_layer": (
         ctypes.c_int,
         (ctypes.POINTER(LayerWeights), _vp, _i64, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp),
+    ),
+    "uqm_moe_layer_noalloc": (
+        ctypes.c_int,
+        (ctypes.POINTER(LayerWeights), _vp, _i64, _vp, _vp, _vp, _vp, _vp),
     ),
     "uqm_norm_moe_layer": (
         ctypes.c_int,

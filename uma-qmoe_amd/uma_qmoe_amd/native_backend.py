@@ -282,6 +282,25 @@ class HipExtension:
         _native.check(rc, "uqm_moe_layer")
         return result.reshape(hidden.shape), logits, weights, indices
 
+    def moe_layer_noalloc(self, layer: DeviceExperts, dense: DenseBlock, hidden, top_k, norm_topk_prob=False, *,
+                          out=None, logits=None, weights=None, indices=None):
+        """``moe_layer`` through uqm_moe_layer_noalloc: the library's static
+        scratch array instead of a workspace. Outputs may be passed in, so a
+        caller that cannot allocate passes every tensor."""
+        torch = self.torch
+        self._check_hidden(hidden)
+        x = hidden.reshape(-1, layer.hidden_size).contiguous()
+        t, e = x.shape[0], layer.num_experts
+        out = torch.empty_like(x) if out is None else out
+        logits = torch.empty((t, e), dtype=torch.bfloat16, device=x.device) if logits is None else logits
+        weights = torch.empty((t, top_k), dtype=torch.bfloat16, device=x.device) if weights is None else weights
+        indices = torch.empty((t, top_k), dtype=torch.int64, device=x.device) if indices is None else indices
+        desc = self.layer_descriptor(layer, dense, top_k, norm_topk_prob)
+        rc = self.lib.uqm_moe_layer_noalloc(ctypes.byref(desc), _ptr(x), t, _ptr(out), _ptr(logits), _ptr(weights),
+                                            _ptr(indices), _stream_handle(torch, x.device))
+        _native.check(rc, "uqm_moe_layer_noalloc")
+        return out.reshape(hidden.shape), logits, weights, indices
+
     def norm_moe_layer(self, layer: DeviceExperts, dense: DenseBlock, hidden, top_k, eps=1e-6, norm_weight=None,
                        norm_topk_prob=False, *, out=None, workspace=None):
         """MoE block on RMSNorm(hidden) (eps, bf16 weight [H] or None for ones).
