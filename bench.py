@@ -37,10 +37,12 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=24)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "trace"],
                     help="c2 (default): Qwen W4A16 decode; c1: OLMoE decode; c3: 24-layer Qwen stack (BF16/Q8 routed "
                          "experts), decode; c4: Qwen prefill, 512 tokens; c5: 128-expert top-8 layer, 256 tokens "
-                         "with Zipf-skewed routes (routed experts only)")
+                         "with Zipf-skewed routes (routed experts only); trace: the reference's measured OLMoE "
+                         "RouteTrace (128-token prefill + 31 decode tokens over 16 layers) replayed through "
+                         "c1-shaped Q4 layers")
     ap.add_argument("--tokens", type=int, default=0, help="tokens per call (0: the config's own)")
     ap.add_argument("--rotate-bytes", type=float, default=1.1e9)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -502,6 +504,99 @@ def main_stack(args, torch, syn, ext) -> int:
     return 0
 
 
+TRACE_FIXTURE = ROOT / "tests" / "golden" / "route_trace" / "olmoe_1b_7b_0125_128x32_greedy_v1.npz"
+
+
+def main_trace(args, torch, syn, ext) -> int:
+    """Replays the measured routes of the reference's RouteTrace (OLMoE,
+    batch 1, 128 prompt tokens, 32 output tokens: one prefill event, 31
+    decode events) through 16 synthetic c1-shaped Q4 layers: each (event,
+    layer) is one routed-expert call with the trace's expert ids and routing
+    weights. The prefill (16 calls of 128 tokens) and the decode steps (31 x
+    16 single-token calls) are captured in two HIP graphs and timed apart;
+    algorithmic bytes count each distinct expert of an (event, layer) once
+    (16 x 64 experts x 3.34 MB = 3.4 GB of layers, no rotation needed)."""
+    from uma_qmoe_amd.route_trace import distinct_experts, load_arrays
+
+    arrays = load_arrays(TRACE_FIXTURE)
+    dev = torch.device("cuda:0")
+    shape = syn.C1
+    n_layers = arrays["expert_indices"].shape[0]
+    progress(f"trace: building {n_layers} c1 layers")
+    layers = [syn.build_experts(shape, layer=l, device=dev) for l in range(n_layers)]
+    counts = [int(c) for c in arrays["token_counts"]]
+    bounds = [0]
+    for c in counts:
+        bounds.append(bounds[-1] + c)
+    idx = torch.from_numpy(arrays["expert_indices"]).to(dev)
+    wts = torch.from_numpy(arrays["routing_weights"]).to(torch.bfloat16).to(dev)
+    xs = [syn.hidden_states(shape, c, device=dev, tag=f"trace{e}") for e, c in enumerate(counts)]
+    outs = [torch.empty_like(x) for x in xs]
+    ws = ext._workspace(dev, max(counts), shape.hidden, shape.intermediate, 0, shape.num_experts, shape.top_k)
+
+    def run(events):
+        for e in events:
+            for l in range(n_layers):
+                ext.moe_forward(layers[l], xs[e], idx[l, bounds[e]:bounds[e + 1]], wts[l, bounds[e]:bounds[e + 1]],
+                                out=outs[e], workspace=ws)
+
+    prefill, decode = [0], list(range(1, len(counts)))
+    run(prefill + decode)
+    torch.cuda.synchronize()
+    graphs = {}
+    for name, evs in (("prefill", prefill), ("decode", decode)):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run(evs)
+        graphs[name] = g
+    torch.cuda.synchronize()
+    progress("trace: graphs captured")
+    per_expert = layers[0].bytes_per_expert()
+    dist = distinct_experts(arrays)
+    res = {}
+    for name, evs in (("prefill", prefill), ("decode", decode)):
+        # 20 timings of one whole replay each (the decode graph is 496 calls)
+        ms = timed_samples(torch, lambda n, g=graphs[name]: [g.replay() for _ in range(n)], 1, 2, 20)
+        stats = sample_stats([v * 1000.0 for v in ms])
+        nbytes = int(sum(dist[e].sum() for e in evs) * per_expert)
+        res[name] = {"us": stats["p50_us"], "bytes": nbytes, "stats": stats}
+        progress(f"trace {name}: {stats['p50_us']} us ({len(evs)} events x {n_layers} layers)")
+    dec = res["decode"]
+    us_token = dec["us"] / len(decode)
+    gbps = dec["bytes"] / (dec["us"] * 1e-6) / 1e9
+    pre_gbps = res["prefill"]["bytes"] / (res["prefill"]["us"] * 1e-6) / 1e9
+    line = {
+        "metric": "RouteTrace replay: routed-expert µs per decode token over 16 OLMoE-shaped W4A16 MoE layers",
+        "value": round(us_token, 3),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": len(decode) * n_layers,
+        "warmup": 2 * len(decode) * n_layers,
+        "ms_per_step": round(dec["us"] / (len(decode) * n_layers) / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w4a16 (q4 weights, bf16 activations, fp32 accumulate)",
+        "data": "routes measured by the reference (benchmarks/traces/olmoe_1b_7b_0125_128x32_greedy_v1.json, "
+                "stored as tests/golden/route_trace/*.npz); synthetic N(0,0.02) weights and N(0,1) hidden states",
+        "config": {"workload": "trace: 16 c1-shaped Q4 layers (E 64, top-8, I 1024, H 2048), routed experts only, "
+                               "one 128-token prefill event and 31 single-token decode events",
+                   "parallelism": "single GPU"},
+        "us_per_layer_call": round(dec["us"] / (len(decode) * n_layers), 3),
+        "decode": {"us_all_steps": round(dec["us"], 3), "algorithmic_bytes": dec["bytes"],
+                   "hbm_gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4), "timing": dec["stats"]},
+        "prefill": {"us": round(res["prefill"]["us"], 3), "tokens": counts[0], "algorithmic_bytes": res["prefill"]["bytes"],
+                    "hbm_gbps": round(pre_gbps, 1), "frac": round(pre_gbps / HBM_PEAK_GBPS, 4),
+                    "distinct_experts_per_layer": [int(v) for v in dist[0]], "timing": res["prefill"]["stats"]},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+    }
+    ext.workspace_status(ws)
+    progress("done")
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def workload_name(shape) -> str:
     enc = {"q4_group128": "Q4", "q8_group128": "Q8", "bf16_le": "BF16"}[shape.encoding]
     w = (f"{shape.name}: one MoE block (router + top-{shape.top_k} of {shape.num_experts} {enc} experts "
@@ -538,6 +633,8 @@ def main() -> int:
     _platform, ext = load_native_extension()
     if args.config == "c3":
         return main_stack(args, torch, syn, ext)
+    if args.config == "trace":
+        return main_trace(args, torch, syn, ext)
     if args.multi_kernel:
         ext.set_option(_native.UQM_OPT_FUSED_DECODE, 0)
     shape = syn.CONFIGS[args.config]
