@@ -152,7 +152,10 @@ int uqm_router_topk(const void* hidden, int64_t tokens, int64_t hidden_size, con
  * Replaces q4_moe_forward / q4_moe_prefill / q8_moe_forward / q8_moe_prefill
  * (src/uma_qmoe/native/packed_q4_binding.cpp:197-488, 490-515) and the Python
  * per-expert Qwen loops (src/uma_qmoe/native_backend.py:319-372, 722-753) and
- * the BF16 grouped_mm path (:958-1005). Any E, k, H, I; any token count. */
+ * the BF16 grouped_mm path (:958-1005). Any E, k, H, I; any token count. One
+ * or two tokens of a shape the fused kernel covers (see uqm_moe_layer) run as
+ * one persistent launch per token with these routes; expert ids outside
+ * [0, E) contribute nothing on every path. */
 int uqm_moe_forward(const uqm_expert_weights* weights, const void* hidden, int64_t tokens,
                     const int64_t* expert_indices, const void* routing_weights, int64_t top_k, void* output,
                     void* workspace, size_t workspace_bytes, void* stream);

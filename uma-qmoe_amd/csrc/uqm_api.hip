@@ -643,6 +643,39 @@ int uqm_moe_forward(const uqm_expert_weights* weights, const void* hidden, int64
     return fail(UQM_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required (or misaligned)",
                 workspace_bytes, L.total);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t H = weights->hidden_size, I = weights->intermediate_size, E = weights->num_experts;
+  // One or two tokens: the fused single-token kernel with the caller's routes
+  // (no router), one launch per token.
+  if (tokens <= kFusedMaxTokens && g_opt_fused.load(std::memory_order_relaxed) != 0 &&
+      fused_config_id(weights->encoding, H, I, 0, top_k, E) >= 0 &&
+      (weights->encoding == UQM_BF16 || (H % weights->group_size == 0 && I % weights->group_size == 0))) {
+    FusedArgs fa{};
+    fa.eg = static_cast<const uint8_t*>(weights->gate);
+    fa.eu = static_cast<const uint8_t*>(weights->up);
+    fa.ed = static_cast<const uint8_t*>(weights->down);
+    fa.egs = weights->gate_scales;
+    fa.eus = weights->up_scales;
+    fa.eds = weights->down_scales;
+    fa.H = H;
+    fa.I = I;
+    fa.Is = 0;
+    fa.E = static_cast<int>(E);
+    fa.k = static_cast<int>(top_k);
+    fa.group = weights->encoding == UQM_BF16 ? 1 : weights->group_size;
+    fa.wait_ticks = fused_wait_ticks();
+    fa.sync = at<uint32_t>(workspace, L.fused_sync);
+    fa.hs = at<uint32_t>(workspace, L.fused_hs);
+    fa.hr = at<uint32_t>(workspace, L.fused_hr);
+    fa.lgt = at<uint64_t>(workspace, L.fused_lgt);
+    for (int64_t t = 0; t < tokens; ++t) {
+      fa.x = static_cast<const uint16_t*>(hidden) + t * H;
+      fa.out = static_cast<uint16_t*>(output) + t * H;
+      fa.routes_in = expert_indices + t * top_k;
+      fa.weights_in = static_cast<const uint16_t*>(routing_weights) + t * top_k;
+      if ((rc = hip_check(launch_moe_decode_fused(weights->encoding, fa, s), "fused routed launch"))) return rc;
+    }
+    return UQM_OK;
+  }
   RouteTables rt{at<int32_t>(workspace, L.route_expert), at<int32_t>(workspace, L.route_order),
                  at<int32_t>(workspace, L.expert_offsets), at<int32_t>(workspace, L.active_experts),
                  at<int32_t>(workspace, L.counters), at<int32_t>(workspace, L.tiles),

@@ -17,6 +17,9 @@
 //      y_r[o] = sum_k w_k * (down_ek row o . h_k), summed in the same wave:
 //      out[o] = bf16(sigmoid(x . w_g) * y_s[o] + y_r[o]).
 //
+// The routed-only ops pass their routes in (routes_in / weights_in): the
+// control wave then loads the k ids and weights instead of routing.
+//
 // Routing runs beside phase A: the router rows (plus the shared expert's gate
 // row) are spread over the workgroups, one row each, and published; the
 // control wave of every workgroup polls the published logits, runs the
@@ -470,6 +473,36 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     // Routing is on every wave's critical path: its instructions go first
     // when it shares a SIMD with streaming waves.
     __builtin_amdgcn_s_setprio(UQM_FUSED_CTRL_PRIO);
+    // After the routes are in LDS: the workgroup's barriers, the routed
+    // fragments, and the epoch advanced for the next launch.
+    auto finish_control = [&](uint32_t epoch) {
+      UQM_FUSED_TRACE(3);
+      lds_barrier();  // routes ready
+      lds_barrier();  // routed gate/up rows issued
+      lds_barrier();  // shared products staged
+      lds_barrier();  // routed products staged
+      build_fragments();
+      lds_barrier();  // routed fragments built
+      if (lane == 0) co_store<uint32_t>(my_epoch, epoch);
+    };
+    if (a.routes_in != nullptr) {
+      // Routes given by the caller (the routed-only ops, no shared expert):
+      // no router and no logit poll. An id outside [0, E) contributes
+      // nothing (weight 0, expert 0 read in its place).
+      const uint32_t last_epoch = co_load(my_epoch + opaque_zero());
+      if (lane < k) {
+        const int64_t r = a.routes_in[lane];
+        const bool ok = r >= 0 && r < E;
+        l_route[lane] = ok ? static_cast<int>(r) : 0;
+        l_w[lane] = ok ? bf16_to_f32(a.weights_in[lane]) : 0.f;
+      }
+      if (lane == 0) {
+        *l_bad = 0;
+        *l_stale = 0;
+      }
+      finish_control(next_epoch(last_epoch));
+      return;
+    }
     // Activation, epoch and router row loads go out together: one round trip.
     XRaw<kBF16, CH> x_raw, w_raw;
     load_x<kBF16, CH>(a.x, colH16, x_raw);
@@ -616,21 +649,14 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
           if (lane + 64 * j < E) a.logits_out[lane + 64 * j] = f32_to_bf16(lv[j]);
       }
     }
-    UQM_FUSED_TRACE(3);
-    lds_barrier();  // routes ready
-    lds_barrier();  // routed gate/up rows issued
-    lds_barrier();  // shared products staged
-    lds_barrier();  // routed products staged
-    build_fragments();
-    lds_barrier();  // routed fragments built
-    if (lane == 0) co_store<uint32_t>(my_epoch, epoch);
+    finish_control(epoch);
     return;
   }
 
   // ======================================================= streaming waves
   // In the workgroups that compute a router row, the streaming waves let the
   // control wave's loads go first, so that routing is not queued behind them.
-  if (b < nrow) __builtin_amdgcn_s_sleep(kRouterHeadStart);
+  if (a.routes_in == nullptr && b < nrow) __builtin_amdgcn_s_sleep(kRouterHeadStart);
   const int sw = b * kWaves + wave, nsw = nb * kWaves;
   Cols<ENC, CHR> colHR;
   make_cols<ENC, CHR>(H / ER::kElems, group, colHR);

@@ -163,6 +163,10 @@ struct FusedArgs {
   uint16_t* logits_out;                // optional [E]
   uint16_t* weights_out;               // optional [k]
   int64_t* indices_out;                // optional [k]
+  // Routes given by the caller (routed-only ops, no shared expert): expert
+  // ids [k] and bf16 routing weights [k]; NULL: the kernel routes itself.
+  const int64_t* routes_in;
+  const uint16_t* weights_in;
 };
 
 // Returns >= 0 when a compiled instantiation covers (encoding, H, I, Is, k, E).
