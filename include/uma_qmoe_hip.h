@@ -60,10 +60,13 @@ enum {
                                   kernel, one launch per token */
   UQM_OPT_MFMA_MIN_TOKENS = 3,     /* token count from which multi-token calls run the expert projections
                                       as MFMA grouped GEMMs (default 2; 0 = never, batched GEMV instead) */
-  UQM_OPT_OVERLAP_SHARED = 4       /* 1 (default): multi-token blocks run the shared expert on a
+  UQM_OPT_OVERLAP_SHARED = 4,      /* 1 (default): multi-token blocks run the shared expert on a
                                       library-owned side stream (one per device, default priority),
                                       forked from and joined back into the caller's stream with
                                       events; 0: everything in order on the caller's stream */
+  UQM_OPT_STREAM_MAX_ROUTES = 5    /* multi-token calls with at most this many routes (tokens x top_k;
+                                      default 32, 0 = never) run the routed projections as
+                                      expert-grouped streaming GEMVs instead of MFMA grouped GEMMs */
 };
 
 /* Routed-expert weights of one MoE layer (device pointers). */

@@ -1,6 +1,6 @@
-"""GPU parity of the MFMA grouped-GEMM path (multi-token calls) against the
-CPU oracle and against the batched-GEMV path (a second, independent HIP
-implementation of the same projections).
+"""GPU parity of the MFMA grouped-GEMM path and of the streaming GEMV path
+(multi-token calls) against the CPU oracle and against the workgroup-staged
+batched-GEMV path (independent HIP implementations of the same projections).
 
 Tolerances: rel-L2 <= 1e-2, max-abs <= 2e-2 against the oracle (north star);
 the two HIP paths compute the same FP32 sums in different orders, so their
@@ -77,17 +77,30 @@ def routes(t, k, e, seed, hot=None, hot_share=0.0):
     return idx, w
 
 
+STREAM_DEFAULT = 32  # UQM_OPT_STREAM_MAX_ROUTES default (routes per call)
+STREAM_ALWAYS = 1 << 30
+
+
+def restore_defaults(ext) -> None:
+    ext.set_option(_native.UQM_OPT_MFMA_MIN_TOKENS, 2)
+    ext.set_option(_native.UQM_OPT_FUSED_DECODE, 1)
+    ext.set_option(_native.UQM_OPT_STREAM_MAX_ROUTES, STREAM_DEFAULT)
+
+
 @pytest.fixture
 def mfma_on(hip_ext):
-    # two-token blocks would take the fused kernel once per token
+    # two-token blocks would take the fused kernel once per token; the
+    # streaming GEMV would take the calls with few routes per expert
     hip_ext.set_option(_native.UQM_OPT_MFMA_MIN_TOKENS, 2)
     hip_ext.set_option(_native.UQM_OPT_FUSED_DECODE, 0)
+    hip_ext.set_option(_native.UQM_OPT_STREAM_MAX_ROUTES, 0)
     yield hip_ext
-    hip_ext.set_option(_native.UQM_OPT_MFMA_MIN_TOKENS, 2)
-    hip_ext.set_option(_native.UQM_OPT_FUSED_DECODE, 1)
+    restore_defaults(hip_ext)
 
 
 def both_paths(ext, fn):
+    """(MFMA grouped GEMMs, workgroup-staged GEMV) results of fn."""
+    ext.set_option(_native.UQM_OPT_STREAM_MAX_ROUTES, 0)
     ext.set_option(_native.UQM_OPT_MFMA_MIN_TOKENS, 2)
     a = fn()
     ext.set_option(_native.UQM_OPT_MFMA_MIN_TOKENS, 0)
@@ -95,6 +108,17 @@ def both_paths(ext, fn):
     ext.set_option(_native.UQM_OPT_MFMA_MIN_TOKENS, 2)
     torch.cuda.synchronize()
     return a, b
+
+
+def streamed(ext, fn, threshold=STREAM_ALWAYS):
+    """fn's result with the routed projections on the streaming GEMV."""
+    ext.set_option(_native.UQM_OPT_STREAM_MAX_ROUTES, threshold)
+    try:
+        out = fn()
+        torch.cuda.synchronize()
+    finally:
+        ext.set_option(_native.UQM_OPT_STREAM_MAX_ROUTES, 0)
+    return out
 
 
 @pytest.mark.parametrize("encoding", ["q4_group128", "q8_group128", "bf16_le"])
@@ -113,6 +137,79 @@ def test_routed_matches_oracle_and_gemv(mfma_on, encoding, t):
     ref = om.streaming_reference(x, idx, w, 0, syn.DeviceLayerReader({0: layer}), num_experts=shape.num_experts)
     close(got, ref, f"mfma vs oracle {encoding} t={t}")
     close(got, gemv, f"mfma vs gemv {encoding} t={t}", rel=5e-3, mx=1e-2)
+
+
+@pytest.mark.parametrize("encoding", ["q4_group128", "q8_group128", "bf16_le"])
+@pytest.mark.parametrize("t", [1, 2, 3, 16, 37, 100])
+def test_stream_matches_oracle_and_mfma(mfma_on, encoding, t):
+    """Routed experts on the streaming GEMV (forced for every route count, so
+    experts with more routes than a wave holds take several passes, and rows
+    of 24 chunks leave most lanes idle) against the oracle and the MFMA and
+    staged-GEMV paths."""
+    ext = mfma_on
+    shape = replace(MID, encoding=encoding)
+    note(f"stream routed {encoding} t={t}")
+    layer = syn.build_experts(shape, seed=t)
+    dl = to_dev(layer)
+    x = syn.hidden_states(shape, t, seed=t)
+    idx, w = routes(t, shape.top_k, shape.num_experts, 100 + t)
+    call = lambda: ext.moe_forward(dl, x.to(DEV), idx.to(DEV), w.to(DEV))
+    got = streamed(ext, call)
+    mfma, gemv = both_paths(ext, call)
+    ref = om.streaming_reference(x, idx, w, 0, syn.DeviceLayerReader({0: layer}), num_experts=shape.num_experts)
+    close(got, ref, f"stream vs oracle {encoding} t={t}")
+    close(got, gemv, f"stream vs gemv {encoding} t={t}", rel=5e-3, mx=1e-2)
+    if t >= 2:
+        close(got, mfma, f"stream vs mfma {encoding} t={t}", rel=5e-3, mx=1e-2)
+    # invalid ids contribute nothing on this path too
+    idx2 = idx.clone()
+    idx2[::3, 0] = -1
+    got2 = streamed(ext, lambda: ext.moe_forward(dl, x.to(DEV), idx2.to(DEV), w.to(DEV)))
+    w2 = w.clone()
+    w2[::3, 0] = 0
+    ref2 = om.streaming_reference(x, idx, w2, 0, syn.DeviceLayerReader({0: layer}), num_experts=shape.num_experts)
+    close(got2, ref2, f"stream dropped ids {encoding} t={t}")
+
+
+@pytest.mark.parametrize("t", [3, 5, 8])
+def test_qwen_block_stream_decode(mfma_on, t):
+    """c2 shapes at batch 3, 5 and 8 with the default threshold (at most 32
+    routes, so the streaming GEMV takes the routed experts): against the
+    oracle block and the MFMA path, eagerly and replayed from a HIP graph."""
+    ext = mfma_on
+    shape = syn.C2
+    note(f"stream qwen block t={t}")
+    layer = syn.build_experts(shape, device=DEV)
+    dense = syn.build_dense(shape, device=DEV)
+    x = syn.hidden_states(shape, t, seed=90 + t).to(DEV)
+    out, logits, weights, indices = [v.clone() for v in
+                                     streamed(ext, lambda: ext.moe_layer(layer, dense, x, shape.top_k), STREAM_DEFAULT)]
+    assert_weights_follow_logits(logits, weights, indices, False, f"c2 stream block t={t}")
+    ref, *_ = om.qwen_block(x.cpu(), layout_of(shape, dense_cpu(dense)), syn.DeviceLayerReader({0: layer}), 0,
+                            routes=(weights.cpu(), indices.cpu()))
+    close(out, ref, f"c2 stream block t={t}")
+    mfma = ext.moe_layer(layer, dense, x, shape.top_k)[0]
+    close(out, mfma, f"c2 stream vs mfma t={t}", rel=5e-3, mx=1e-2)
+    ws = torch.zeros(ext.lib.uqm_moe_workspace_bytes(t, shape.hidden, shape.intermediate, shape.shared_intermediate,
+                                                     shape.num_experts, shape.top_k), dtype=torch.uint8, device=DEV)
+    ext.set_option(_native.UQM_OPT_STREAM_MAX_ROUTES, STREAM_DEFAULT)
+    try:
+        res = torch.empty_like(x)
+        ext.moe_layer(layer, dense, x, shape.top_k, out=res, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(res, out), "workspace call"
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            ext.moe_layer(layer, dense, x, shape.top_k, out=res, workspace=ws)
+        for rep in range(3):
+            res.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(res, out), f"graph replay {rep}"
+            ext.moe_layer(layer, dense, x, shape.top_k, workspace=ws)
+        del graph
+    finally:
+        ext.set_option(_native.UQM_OPT_STREAM_MAX_ROUTES, 0)
 
 
 @pytest.mark.parametrize("encoding", ["q4_group128", "bf16_le"])

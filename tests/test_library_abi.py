@@ -58,7 +58,7 @@ def header_enum_values() -> dict[str, int]:
 def test_python_constants_match_header_enums():
     values = header_enum_values()
     for name in ("UQM_Q4", "UQM_Q8", "UQM_BF16", "UQM_OPT_FUSED_DECODE",
-                 "UQM_OPT_MFMA_MIN_TOKENS", "UQM_OPT_OVERLAP_SHARED"):
+                 "UQM_OPT_MFMA_MIN_TOKENS", "UQM_OPT_OVERLAP_SHARED", "UQM_OPT_STREAM_MAX_ROUTES"):
         assert values[name] == getattr(_native, name), name
 
 
@@ -69,6 +69,8 @@ def test_set_option_is_host_only_and_validates():
     assert lib.uqm_set_option(99, 1) != 0
     assert b"unknown option" in lib.uqm_last_error()
     assert lib.uqm_set_option(_native.UQM_OPT_MFMA_MIN_TOKENS, -1) != 0
+    assert lib.uqm_set_option(_native.UQM_OPT_STREAM_MAX_ROUTES, -1) != 0
+    assert lib.uqm_set_option(_native.UQM_OPT_STREAM_MAX_ROUTES, 32) == 0  # the default
 
 
 def test_noalloc_limit_is_checked_on_the_host():

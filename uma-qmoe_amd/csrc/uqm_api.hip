@@ -89,6 +89,7 @@ P* at(void* ws, size_t off) {
 std::atomic<int64_t> g_opt_fused{1};
 std::atomic<int64_t> g_opt_mfma_min_tokens{2};
 std::atomic<int64_t> g_opt_overlap_shared{1};
+std::atomic<int64_t> g_opt_stream_max_routes{32};
 
 // Token counts served by one fused single-token launch per token.
 constexpr int64_t kFusedMaxTokens = 2;
@@ -176,6 +177,14 @@ bool shared_uses_mfma(int64_t H, int64_t Is, int64_t T) {
   return min_t > 0 && T >= min_t && uqm::mfma_supported(UQM_BF16, Is, H, 0) && uqm::mfma_supported(UQM_BF16, H, Is, 0);
 }
 
+// Whether the GEMV path of the routed experts streams (uqm_stream.hip) rather
+// than staging activations per workgroup (uqm_gemv.hip).
+bool routed_uses_stream(const uqm_expert_weights* w) {
+  return g_opt_stream_max_routes.load(std::memory_order_relaxed) > 0 &&
+         uqm::stream_supported(w->encoding, w->hidden_size, w->group_size) &&
+         uqm::stream_supported(w->encoding, w->intermediate_size, w->group_size);
+}
+
 // Route tile size the routed MFMA path uses (0 = GEMV path). From 16 routes
 // per expert on average, 32-route tiles: measured faster than 16 (c5: 80 vs
 // 105 us) and than 64 (c4: 247 vs 271 us), whose 4-wave items take longer per
@@ -185,6 +194,7 @@ int routed_tile_tokens(const uqm_expert_weights* w, int64_t T, int64_t k) {
   const int64_t R = T * k;
   const int64_t active = R < w->num_experts ? R : w->num_experts;
   const double mean = static_cast<double>(R) / static_cast<double>(active);
+  if (routed_uses_stream(w) && R <= g_opt_stream_max_routes.load(std::memory_order_relaxed)) return 0;
   return 16 * (mean >= 16 ? 2 : nb_for(w->encoding, mean));
 }
 
@@ -383,7 +393,12 @@ int run_routed(const uqm_expert_weights* w, const uint16_t* hidden, int64_t T, i
     return hip_check(launch_expert_mfma(w->encoding, 1, d, pd.nb, pd.kw, pd.mw, cus, stream), "down MFMA launch");
   }
   const int grid_y = static_cast<int>(E < R ? E : R);
-  const int nt = static_cast<int>(T < 4 ? T : 4);
+  const bool stream_path = routed_uses_stream(w);
+  // Streaming GEMV: routes per expert held in registers, from the mean routes
+  // per active expert (experts with more take further passes).
+  const int64_t mean_routes = (R + grid_y - 1) / grid_y;
+  const int nt = stream_path ? static_cast<int>(mean_routes <= 1 ? 1 : mean_routes <= 2 ? 2 : 4)
+                             : static_cast<int>(T < 4 ? T : 4);
   GemvArgs g{};
   g.w[0] = static_cast<const uint8_t*>(w->gate);
   g.w[1] = static_cast<const uint8_t*>(w->up);
@@ -401,7 +416,10 @@ int run_routed(const uqm_expert_weights* w, const uint16_t* hidden, int64_t T, i
   g.active_count = at<int32_t>(ws, L.counters);
   g.out = at<uint16_t>(ws, L.h_routed);
   g.ldo = I;
-  int rc = hip_check(launch_expert_gemv(w->encoding, 2, kModeSilu, g, grid_y, nt, stream), "gate/up launch");
+  const int cus = device_cus();
+  int rc = hip_check(stream_path ? launch_routed_stream(w->encoding, 2, kModeSilu, g, nt, grid_y, cus, stream)
+                                 : launch_expert_gemv(w->encoding, 2, kModeSilu, g, grid_y, nt, stream),
+                     "gate/up launch");
   if (rc) return rc;
   GemvArgs d = g;
   d.w[0] = static_cast<const uint8_t*>(w->down);
@@ -415,7 +433,9 @@ int run_routed(const uqm_expert_weights* w, const uint16_t* hidden, int64_t T, i
   d.x_div = 1;
   d.out = at<float>(ws, L.y_routed);
   d.ldo = H;
-  return hip_check(launch_expert_gemv(w->encoding, 1, kModeF32, d, grid_y, nt, stream), "down launch");
+  return hip_check(stream_path ? launch_routed_stream(w->encoding, 1, kModeF32, d, nt, grid_y, cus, stream)
+                               : launch_expert_gemv(w->encoding, 1, kModeF32, d, grid_y, nt, stream),
+                   "down launch");
 }
 
 // Shared expert on T tokens: h_shared = silu(x Wg^T) * (x Wu^T), y_shared =
@@ -954,6 +974,10 @@ int uqm_set_option(int option, int64_t value) {
       return UQM_OK;
     case UQM_OPT_OVERLAP_SHARED:
       g_opt_overlap_shared.store(value != 0 ? 1 : 0);
+      return UQM_OK;
+    case UQM_OPT_STREAM_MAX_ROUTES:
+      if (value < 0) return fail(UQM_ERR_ARGUMENT, "routes threshold must be >= 0");
+      g_opt_stream_max_routes.store(value);
       return UQM_OK;
     default:
       return fail(UQM_ERR_ARGUMENT, "unknown option %d", option);

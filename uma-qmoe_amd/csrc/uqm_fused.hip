@@ -52,6 +52,8 @@
 // registers. Loads are issued branch-free (out-of-row lanes re-read the row's
 // first chunk and are masked in the arithmetic) and all row bookkeeping is
 // wave-uniform, so every load of a batch is in flight before the first wait.
+#include <type_traits>
+
 #include "uqm_internal.h"
 
 // Phase-boundary trace hooks: no-ops here; a timing harness may define them
@@ -77,6 +79,11 @@ constexpr uint16_t kBf16NaN = 0x7FC0;      // poison of products and outputs aft
 constexpr int kPollSleep = 40;             // s_sleep units (64 clocks) between router logit polls
 constexpr int kPollDelay = 64;             // s_sleep units before the first poll (the logits cannot be
                                            // in sooner; fewer polls leave more bandwidth to phase A)
+// Without a shared expert nothing streams while the routes are pending (every
+// streaming wave waits for them), so the polls go out sooner and closer:
+// c1 17.3 vs 18.5 us per call, with one load per poll.
+constexpr int kPollSleepRoutedOnly = 20;
+constexpr int kPollDelayRoutedOnly = 24;
 constexpr int kRouterHeadStart = 12;       // s_sleep units the streaming waves of router workgroups yield
 enum { kNormNone = 0, kNormUnit = 1, kNormWeighted = 2 };  // input RMSNorm: none, weight ones, weight row
 #ifndef UQM_FUSED_CTRL_PRIO
@@ -533,57 +540,71 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     // kept in flight, ~1 us apart, so a late producer is seen one spacing (not
     // one round trip) after it publishes; every poll issues the same loads
     // (lanes past the end re-read the last word), which keeps the compiler's
-    // waits for the oldest poll exact. (All 256 control waves poll the same
-    // few lines: polling more often measurably slows the streaming phases.)
-    uint64_t pa[LPL], pb[LPL], pc[LPL];
-    auto poll = [&](uint64_t (&t)[LPL]) {
-#pragma unroll
-      for (int j = 0; j < LPL; ++j) t[j] = co_load(a.lgt + min(lane + 64 * j, nrow - 1));
-    };
-    auto ready = [&](const uint64_t (&t)[LPL]) {
-      bool ok = true;
-#pragma unroll
-      for (int j = 0; j < LPL; ++j) ok &= static_cast<uint32_t>(t[j] >> 32) == epoch || lane + 64 * j >= nrow;
-      return __all(ok) != 0;
-    };
+    // waits for the oldest poll exact. Without a shared expert a poll is one
+    // load per lane when the rows fit in one (E <= 64); with one, LPL loads
+    // per poll measured faster (c2: 22.5 vs 22.9-23.2 us per call with one).
+    // (All 256 control waves poll the same few lines: polling more often
+    // measurably slows the streaming phases.)
+    constexpr int kDelay = kShared ? kPollDelay : kPollDelayRoutedOnly;
+    constexpr int kSleep = kShared ? kPollSleep : kPollSleepRoutedOnly;
     float lv[LPL];
-    auto take = [&](const uint64_t (&t)[LPL]) {
 #pragma unroll
-      for (int j = 0; j < LPL; ++j) lv[j] = __uint_as_float(static_cast<uint32_t>(t[j]));
-    };
-    __builtin_amdgcn_s_sleep(kPollDelay);
-    poll(pa);
-    __builtin_amdgcn_s_sleep(kPollSleep);
-    poll(pb);
-    __builtin_amdgcn_s_sleep(kPollSleep);
-    poll(pc);
+    for (int j = 0; j < LPL; ++j) lv[j] = 0.f;
     bool bad = false;
-    for (;;) {
-      if (ready(pa)) {
-        take(pa);
-        break;
-      }
-      if (wall_clock() > deadline) {
-        raise_expired(a.sync, epoch);
-        bad = true;
-        take(pa);
-        break;
-      }
+    auto poll_logits = [&](auto loads) {
+      constexpr int L = decltype(loads)::value;
+      uint64_t pa[L], pb[L], pc[L];
+      auto poll = [&](uint64_t (&t)[L]) {
+#pragma unroll
+        for (int j = 0; j < L; ++j) t[j] = co_load(a.lgt + min(lane + 64 * j, nrow - 1));
+      };
+      auto ready = [&](const uint64_t (&t)[L]) {
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < L; ++j) ok &= static_cast<uint32_t>(t[j] >> 32) == epoch || lane + 64 * j >= nrow;
+        return __all(ok) != 0;
+      };
+      auto take = [&](const uint64_t (&t)[L]) {
+#pragma unroll
+        for (int j = 0; j < L; ++j) lv[j] = __uint_as_float(static_cast<uint32_t>(t[j]));
+      };
+      __builtin_amdgcn_s_sleep(kDelay);
       poll(pa);
-      __builtin_amdgcn_s_sleep(kPollSleep);
-      if (ready(pb)) {
-        take(pb);
-        break;
-      }
+      __builtin_amdgcn_s_sleep(kSleep);
       poll(pb);
-      __builtin_amdgcn_s_sleep(kPollSleep);
-      if (ready(pc)) {
-        take(pc);
-        break;
-      }
+      __builtin_amdgcn_s_sleep(kSleep);
       poll(pc);
-      __builtin_amdgcn_s_sleep(kPollSleep);
-    }
+      for (;;) {
+        if (ready(pa)) {
+          take(pa);
+          break;
+        }
+        if (wall_clock() > deadline) {
+          raise_expired(a.sync, epoch);
+          bad = true;
+          take(pa);
+          break;
+        }
+        poll(pa);
+        __builtin_amdgcn_s_sleep(kSleep);
+        if (ready(pb)) {
+          take(pb);
+          break;
+        }
+        poll(pb);
+        __builtin_amdgcn_s_sleep(kSleep);
+        if (ready(pc)) {
+          take(pc);
+          break;
+        }
+        poll(pc);
+        __builtin_amdgcn_s_sleep(kSleep);
+      }
+    };
+    if (!kShared && nrow <= 64)
+      poll_logits(std::integral_constant<int, 1>{});
+    else
+      poll_logits(std::integral_constant<int, LPL>{});
     UQM_FUSED_TRACE(2);
     // FP32 softmax statistics over the E expert logits.
     float mx = -INFINITY;

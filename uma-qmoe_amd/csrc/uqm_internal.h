@@ -45,6 +45,15 @@ hipError_t launch_expert_gemv(int enc, int nmat, int mode, const GemvArgs& a, in
                               hipStream_t stream);
 size_t gemv_lds_bytes(int enc, int64_t K, int nt);
 
+// Expert-grouped streaming GEMV (uqm_stream.hip): a persistent grid splits
+// the (active expert, row) pairs evenly over its waves; activations of up to
+// nt routes of an expert live in registers. Needs route_order,
+// expert_offsets, active_experts and active_count; max_active bounds
+// *active_count (grid sizing only). Writes out[route * ldo + row].
+bool stream_supported(int enc, int64_t K, int64_t group);
+hipError_t launch_routed_stream(int enc, int nmat, int mode, const GemvArgs& a, int nt, int64_t max_active, int cus,
+                                hipStream_t stream);
+
 // Expert-grouped GEMM on the MFMA cores (uqm_mfma.hip). Output block =
 // rows of one expert x one tile of up to 16*nb routes. Matrix m of expert e,
 // row r starts at w[m] + (e * rows + r) * row_bytes; scales as GemvArgs.

@@ -23,6 +23,7 @@ UQM_OPT_FUSED_DECODE = 1
 UQM_OPT_MFMA_MIN_TOKENS = 3
 NOALLOC_SCRATCH_BYTES = 16 << 20  # UQM_NOALLOC_SCRATCH_BYTES
 UQM_OPT_OVERLAP_SHARED = 4
+UQM_OPT_STREAM_MAX_ROUTES = 5
 
 ENCODING_IDS = {"q4_group128": UQM_Q4, "q8_group128": UQM_Q8, "bf16_le": UQM_BF16}
 
