@@ -282,8 +282,12 @@ def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
         probe_bytes = syn.algorithmic_bytes(probe, dense0, int(torch.unique(probe_idx).numel()))
     r_inst = max(2, math.ceil(rotate_bytes / probe_bytes))
     progress(f"{shape.name} T={tokens}: building {r_inst} layer instances")
-    layers = [probe] + [syn.build_experts(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
-    denses = [dense0] + [syn.build_dense(shape, device=dev, seed=syn.SEED + 100 + i) for i in range(r_inst - 1)]
+    layers, denses = [probe], [dense0]
+    for i in range(r_inst - 1):
+        layers.append(syn.build_experts(shape, device=dev, seed=syn.SEED + 100 + i))
+        denses.append(syn.build_dense(shape, device=dev, seed=syn.SEED + 100 + i))
+        torch.cuda.synchronize()
+        progress(f"{shape.name} T={tokens}: instance {i + 2}/{r_inst} built")
     outs = [torch.empty((tokens, shape.hidden), dtype=torch.bfloat16, device=dev) for _ in range(r_inst)]
 
     def run_range(n):
@@ -299,7 +303,9 @@ def measure(torch, syn, ext, shape, tokens, steps, warmup, rotate_bytes):
     # eager warm-up; a fused launch that hit its wait budget (workgroups not
     # all resident) raises here instead of being timed
     results = run_range(r_inst)
+    torch.cuda.synchronize()
     ext.workspace_status(ws)
+    progress(f"{shape.name} T={tokens}: eager pass done")
     results = run_range(r_inst)
     torch.cuda.synchronize()
     distinct = [int(torch.unique(res[3]).numel()) for res in results]

@@ -540,39 +540,31 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     // kept in flight, ~1 us apart, so a late producer is seen one spacing (not
     // one round trip) after it publishes; every poll issues the same loads
     // (lanes past the end re-read the last word), which keeps the compiler's
-    // waits for the oldest poll exact. Without a shared expert a poll is one
-    // load per lane when the rows fit in one (E <= 64); with one, LPL loads
-    // per poll measured faster (c2: 22.5 vs 22.9-23.2 us per call with one).
-    // (All 256 control waves poll the same few lines: polling more often
-    // measurably slows the streaming phases.)
-    constexpr int kDelay = kShared ? kPollDelay : kPollDelayRoutedOnly;
-    constexpr int kSleep = kShared ? kPollSleep : kPollSleepRoutedOnly;
+    // waits for the oldest poll exact. (All 256 control waves poll the same
+    // few lines: polling more often measurably slows the streaming phases.)
     float lv[LPL];
-#pragma unroll
-    for (int j = 0; j < LPL; ++j) lv[j] = 0.f;
     bool bad = false;
-    auto poll_logits = [&](auto loads) {
-      constexpr int L = decltype(loads)::value;
-      uint64_t pa[L], pb[L], pc[L];
-      auto poll = [&](uint64_t (&t)[L]) {
+    if constexpr (kShared) {
+      uint64_t pa[LPL], pb[LPL], pc[LPL];
+      auto poll = [&](uint64_t (&t)[LPL]) {
 #pragma unroll
-        for (int j = 0; j < L; ++j) t[j] = co_load(a.lgt + min(lane + 64 * j, nrow - 1));
+        for (int j = 0; j < LPL; ++j) t[j] = co_load(a.lgt + min(lane + 64 * j, nrow - 1));
       };
-      auto ready = [&](const uint64_t (&t)[L]) {
+      auto ready = [&](const uint64_t (&t)[LPL]) {
         bool ok = true;
 #pragma unroll
-        for (int j = 0; j < L; ++j) ok &= static_cast<uint32_t>(t[j] >> 32) == epoch || lane + 64 * j >= nrow;
+        for (int j = 0; j < LPL; ++j) ok &= static_cast<uint32_t>(t[j] >> 32) == epoch || lane + 64 * j >= nrow;
         return __all(ok) != 0;
       };
-      auto take = [&](const uint64_t (&t)[L]) {
+      auto take = [&](const uint64_t (&t)[LPL]) {
 #pragma unroll
-        for (int j = 0; j < L; ++j) lv[j] = __uint_as_float(static_cast<uint32_t>(t[j]));
+        for (int j = 0; j < LPL; ++j) lv[j] = __uint_as_float(static_cast<uint32_t>(t[j]));
       };
-      __builtin_amdgcn_s_sleep(kDelay);
+      __builtin_amdgcn_s_sleep(kPollDelay);
       poll(pa);
-      __builtin_amdgcn_s_sleep(kSleep);
+      __builtin_amdgcn_s_sleep(kPollSleep);
       poll(pb);
-      __builtin_amdgcn_s_sleep(kSleep);
+      __builtin_amdgcn_s_sleep(kPollSleep);
       poll(pc);
       for (;;) {
         if (ready(pa)) {
@@ -586,25 +578,81 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
           break;
         }
         poll(pa);
-        __builtin_amdgcn_s_sleep(kSleep);
+        __builtin_amdgcn_s_sleep(kPollSleep);
         if (ready(pb)) {
           take(pb);
           break;
         }
         poll(pb);
-        __builtin_amdgcn_s_sleep(kSleep);
+        __builtin_amdgcn_s_sleep(kPollSleep);
         if (ready(pc)) {
           take(pc);
           break;
         }
         poll(pc);
-        __builtin_amdgcn_s_sleep(kSleep);
+        __builtin_amdgcn_s_sleep(kPollSleep);
       }
-    };
-    if (!kShared && nrow <= 64)
-      poll_logits(std::integral_constant<int, 1>{});
-    else
-      poll_logits(std::integral_constant<int, LPL>{});
+    } else {
+      // Without a shared expert nothing streams while the routes are
+      // pending, so the polls go sooner and closer: one load per lane when
+      // the rows fit in one (E <= 64), else LPL. (Written separately from the
+      // shared-expert case above: folding both into one routine changed the
+      // c2 kernel's code and cost it 0.4 us per call.)
+      auto poll_logits = [&](auto loads) {
+        constexpr int L = decltype(loads)::value;
+        uint64_t pa[L], pb[L], pc[L];
+        auto poll = [&](uint64_t (&t)[L]) {
+#pragma unroll
+          for (int j = 0; j < L; ++j) t[j] = co_load(a.lgt + min(lane + 64 * j, nrow - 1));
+        };
+        auto ready = [&](const uint64_t (&t)[L]) {
+          bool ok = true;
+#pragma unroll
+          for (int j = 0; j < L; ++j) ok &= static_cast<uint32_t>(t[j] >> 32) == epoch || lane + 64 * j >= nrow;
+          return __all(ok) != 0;
+        };
+        auto take = [&](const uint64_t (&t)[L]) {
+#pragma unroll
+          for (int j = 0; j < LPL; ++j) lv[j] = j < L ? __uint_as_float(static_cast<uint32_t>(t[j < L ? j : 0])) : 0.f;
+        };
+        __builtin_amdgcn_s_sleep(kPollDelayRoutedOnly);
+        poll(pa);
+        __builtin_amdgcn_s_sleep(kPollSleepRoutedOnly);
+        poll(pb);
+        __builtin_amdgcn_s_sleep(kPollSleepRoutedOnly);
+        poll(pc);
+        for (;;) {
+          if (ready(pa)) {
+            take(pa);
+            break;
+          }
+          if (wall_clock() > deadline) {
+            raise_expired(a.sync, epoch);
+            bad = true;
+            take(pa);
+            break;
+          }
+          poll(pa);
+          __builtin_amdgcn_s_sleep(kPollSleepRoutedOnly);
+          if (ready(pb)) {
+            take(pb);
+            break;
+          }
+          poll(pb);
+          __builtin_amdgcn_s_sleep(kPollSleepRoutedOnly);
+          if (ready(pc)) {
+            take(pc);
+            break;
+          }
+          poll(pc);
+          __builtin_amdgcn_s_sleep(kPollSleepRoutedOnly);
+        }
+      };
+      if (nrow <= 64)
+        poll_logits(std::integral_constant<int, 1>{});
+      else
+        poll_logits(std::integral_constant<int, LPL>{});
+    }
     UQM_FUSED_TRACE(2);
     // FP32 softmax statistics over the E expert logits.
     float mx = -INFINITY;
