@@ -32,8 +32,9 @@
 // holds token l%16, rows 4*(l/16)+i. The K elements a lane feeds each MFMA
 // follow the order of its 16-byte weight slots; A and B use the same order,
 // so the sum is unchanged. Activation rows are stored in LDS with their
-// 16-byte slots XOR-swizzled by the token index, so the B reads of 16 tokens
-// hit distinct banks.
+// 16-byte slots reordered (the slot a lane of quadrant q reads at K-step S
+// sits at position q + 4 S) and XOR-swizzled by the token index, so the B
+// reads of all 64 lanes hit distinct banks (b_position).
 //
 // Work tiles come from the device-built tile list (expert, first route).
 #include <atomic>
@@ -115,14 +116,22 @@ __device__ __forceinline__ bf16x8_t a_frag(const uint4 (&v)[MEnc<ENC>::kLoads]) 
   return __builtin_bit_cast(bf16x8_t, o);
 }
 
-// Element offset (within a chunk) of the B operand of K-step S for lane
-// quadrant q, matching a_frag's order.
-template <int ENC, int S>
-__device__ __forceinline__ int b_offset(int q) {
-  if constexpr (ENC == kQ4) return 32 * q + 8 * S;
-  else if constexpr (ENC == kQ8) return 64 * (S >> 1) + 16 * q + 8 * (S & 1);
-  else return 32 * S + 8 * q;
+// 16-byte slot (8 elements, within a chunk) of the B operand of K-step S for
+// lane quadrant q, matching a_frag's order.
+template <int ENC>
+__device__ __forceinline__ int b_slot(int q, int S) {
+  if constexpr (ENC == kQ4) return 4 * q + S;
+  else if constexpr (ENC == kQ8) return 8 * (S >> 1) + 2 * q + (S & 1);
+  else return 4 * S + q;
 }
+
+// LDS position of that slot in a staged activation row: q + 4 S, XOR-ed with
+// the row's token index. Reads of one K-step then have q in the low two bits
+// of the position, which the gfx950 LDS serves without bank conflicts for all
+// 64 lanes; with q in bits 2-3 (the chunk order of a Q4 fragment) half of the
+// LDS cycles of the batch-32 Q4 kernels were bank-conflict stalls (rocprofv3
+// SQ_LDS_BANK_CONFLICT), and a probe of both patterns on their own confirms it.
+__device__ __forceinline__ int b_position(int q, int S, int row, int spr) { return (q + 4 * S) ^ (row & (spr - 1)); }
 
 // s_waitcnt with only vmcnt limited (gfx9 encoding: vmcnt bits 3:0 and 15:14).
 template <int N>
@@ -305,7 +314,10 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
         const int xi = k * NL + lw;
         const int r = xi * (1024 / C::ROWB) + lane / C::SPR;  // staged row = kwi * NTOK + tok
         const int tok = r % NTOK;
-        const int slot = (lane % C::SPR) ^ (r & (C::SPR - 1));
+        // this lane fills LDS position lane % SPR of row r: the slot whose
+        // (q, S) b_position maps there
+        const int u = (lane % C::SPR) ^ (r & (C::SPR - 1));
+        const int slot = b_slot<ENC>(u & 3, u >> 2);
         const int route = m[4 + tok];
         xsrc[k] = reinterpret_cast<const uint8_t*>(a.x + static_cast<int64_t>(route / a.x_div) * a.ldx) + slot * 16;
         xkw[k] = r / NTOK;
@@ -408,7 +420,7 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
       }
       auto kstep = [&](auto s_tag) {
         constexpr int S_ = decltype(s_tag)::value;
-        const int slot = (b_offset<ENC, S_>(q) >> 3) ^ (t16 & (C::SPR - 1));
+        const int slot = b_position(q, S_, t16, C::SPR);
         bf16x8_t bfr[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
