@@ -37,12 +37,13 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=24)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "trace"],
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "trace", "qwen"],
                     help="c2 (default): Qwen W4A16 decode; c1: OLMoE decode; c3: 24-layer Qwen stack (BF16/Q8 routed "
                          "experts), decode; c4: Qwen prefill, 512 tokens; c5: 128-expert top-8 layer, 256 tokens "
                          "with Zipf-skewed routes (routed experts only); trace: the reference's measured OLMoE "
                          "RouteTrace (128-token prefill + 31 decode tokens over 16 layers) replayed through "
-                         "c1-shaped Q4 layers")
+                         "c1-shaped Q4 layers; qwen: end-to-end greedy decode of a Qwen1.5-MoE-A2.7B-shaped model "
+                         "(synthetic weights) through the host integration, one HIP graph per token")
     ap.add_argument("--tokens", type=int, default=0, help="tokens per call (0: the config's own)")
     ap.add_argument("--rotate-bytes", type=float, default=1.1e9)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -513,6 +514,113 @@ def main_stack(args, torch, syn, ext) -> int:
 TRACE_FIXTURE = ROOT / "tests" / "golden" / "route_trace" / "olmoe_1b_7b_0125_128x32_greedy_v1.npz"
 
 
+def qwen_config():
+    """Transformers config of Qwen1.5-MoE-A2.7B (its config.json: 24 layers,
+    hidden 2048, 16 heads, 60 routed experts of 1408, top-4, shared expert
+    5632, vocabulary 151936)."""
+    from transformers import Qwen2MoeConfig
+
+    return Qwen2MoeConfig(vocab_size=151936, hidden_size=2048, intermediate_size=5632, moe_intermediate_size=1408,
+                          shared_expert_intermediate_size=5632, num_hidden_layers=24, num_attention_heads=16,
+                          num_key_value_heads=16, num_experts=60, num_experts_per_tok=4, norm_topk_prob=False,
+                          max_position_embeddings=8192, rope_theta=1000000.0, rms_norm_eps=1e-6,
+                          tie_word_embeddings=False, decoder_sparse_step=1, mlp_only_layers=[])
+
+
+def main_qwen(args, torch, syn, ext) -> int:
+    """Greedy decode of a Qwen1.5-MoE-A2.7B-shaped model with synthetic
+    weights (dense BF16 tensors N(0, 0.02), norms 1; routed experts the
+    synthetic Q4 layers of c2, one per layer) through the host integration:
+    every MoE block one ``moe_block`` op over a registered pack, attention and
+    head in torch, the whole step captured in one HIP graph per token over a
+    static KV cache (uma_qmoe_amd.qwen_host). Times ``--steps`` tokens per
+    sample after a 128-token prompt; the reference quotes 94.6 ms TPOT for
+    its eager host on a gfx1151 APU with the real checkpoint,
+    which is not this hardware nor these weights, so vs_baseline is null."""
+    from uma_qmoe_amd.custom_op import register_expert_pack, register_moe_forward, unregister_expert_pack
+    from uma_qmoe_amd.native_backend import install_packed_q4_backend
+    from uma_qmoe_amd.qwen_host import DecodeGraph, replace_moe_blocks, restore_nonpersistent_buffers
+    from transformers import Qwen2MoeForCausalLM
+
+    dev = torch.device("cuda:0")
+    config = qwen_config()
+    layers = config.num_hidden_layers
+    progress(f"qwen: building {layers} synthetic Q4 layers")
+    reader = syn.DeviceLayerReader({l: syn.build_experts(syn.C2, layer=l, device=dev) for l in range(layers)},
+                                   model={"num_experts": config.num_experts})
+    register_moe_forward()
+    install_packed_q4_backend()
+    handle = register_expert_pack(reader)
+    try:
+        with torch.device("meta"):
+            model = Qwen2MoeForCausalLM(config).to(torch.bfloat16)
+        replace_moe_blocks(model, handle, performance_mode=True)
+        model.to_empty(device=dev)
+        gen = torch.Generator(device=dev).manual_seed(syn.SEED)
+        with torch.no_grad():
+            for name, p in model.named_parameters():
+                if name.endswith("norm.weight") or "layernorm" in name:
+                    p.fill_(1.0)
+                else:
+                    p.normal_(0.0, 0.02, generator=gen)
+        restore_nonpersistent_buffers(model, config, dev)
+        model.eval()
+        # a 128-token prompt and a few hundred generated tokens: the static
+        # cache (which attention reads whole every step) stays short
+        prompt_len, samples = 128, 5
+        per_sample = max(1, min(args.steps, 32))
+        warmup = max(1, min(args.warmup, 8))
+        dg = DecodeGraph(model, max_len=prompt_len + 8 + warmup + samples * per_sample + 2)
+        ids = torch.randint(0, config.vocab_size, (1, prompt_len), generator=gen, device=dev)
+        progress("qwen: prefill (stages every layer's experts)")
+        dg.prefill(ids)
+        torch.cuda.synchronize()
+        # eager decode for comparison (same operations, launched one by one)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(2):
+            dg.step_eager()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(4):
+            dg.step_eager()
+        e1.record()
+        torch.cuda.synchronize()
+        eager_ms = e0.elapsed_time(e1) / 4
+        progress(f"qwen: eager decode {eager_ms:.3f} ms/token; capturing")
+        dg.capture()
+        for _ in range(warmup):
+            dg.replay()
+        torch.cuda.synchronize()
+        per_token = []
+        for _ in range(samples):
+            e0.record()
+            for _ in range(per_sample):
+                dg.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            per_token.append(e0.elapsed_time(e1) / per_sample)
+        stats = sample_stats([v * 1000.0 for v in per_token])
+        ms = stats["p50_us"] / 1000.0
+        progress(f"qwen: graph decode {ms:.3f} ms/token, cv {stats['cv']}")
+        line = {
+            "metric": "Qwen1.5-MoE-A2.7B-shaped greedy decode TPOT (ms/token), synthetic weights, HIP graph per token",
+            "value": round(ms, 4), "unit": "ms/token", "n_gpus": 1, "steps": samples * per_sample, "warmup": warmup,
+            "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+            "dtype": "w4a16 routed experts, bf16 dense", "data": "synthetic (random weights, random 128-token prompt)",
+            "config": {"workload": "qwen: 24 x (attention + moe_block), vocab 151936, prompt 128, static KV cache",
+                       "tokens": 1, "parallelism": "single GPU"},
+            "tokens_per_s": round(1000.0 / ms, 2),
+            "eager_ms_per_token": round(eager_ms, 4),
+            "timing": {**stats, "steps_per_sample": per_sample},
+            "reference_tpot_ms": {"value": 94.6, "hardware": "gfx1151 (the reference's eager host, real weights)"},
+        }
+        progress("done")
+        print(json.dumps(line), flush=True)
+        return 0
+    finally:
+        unregister_expert_pack(handle)
+
+
 def main_trace(args, torch, syn, ext) -> int:
     """Replays the measured routes of the reference's RouteTrace (OLMoE,
     batch 1, 128 prompt tokens, 32 output tokens: one prefill event, 31
@@ -639,6 +747,8 @@ def main() -> int:
     _platform, ext = load_native_extension()
     if args.config == "c3":
         return main_stack(args, torch, syn, ext)
+    if args.config == "qwen":
+        return main_qwen(args, torch, syn, ext)
     if args.config == "trace":
         return main_trace(args, torch, syn, ext)
     if args.multi_kernel:

@@ -161,6 +161,12 @@ class HipExtension:
         with self._ws_lock:
             ws = self._ws_cache.get(key)
             if ws is None or ws.numel() < n:
+                # Zero-filling inside a HIP-graph capture would record the
+                # fill, and every replay would reset the fused kernel's launch
+                # epochs (stale hand-offs would then look current).
+                if torch.cuda.is_current_stream_capturing():
+                    raise RuntimeError("uma_qmoe workspace would be allocated inside a HIP-graph capture: run one "
+                                       "call of this shape on the capture stream before capturing")
                 ws = torch.zeros(n, dtype=torch.uint8, device=dev)
                 self._ws_cache[key] = ws
             return ws
