@@ -37,13 +37,14 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=240)
     ap.add_argument("--warmup", type=int, default=24)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "trace", "qwen"],
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "trace", "qwen", "pack"],
                     help="c2 (default): Qwen W4A16 decode; c1: OLMoE decode; c3: 24-layer Qwen stack (BF16/Q8 routed "
                          "experts), decode; c4: Qwen prefill, 512 tokens; c5: 128-expert top-8 layer, 256 tokens "
                          "with Zipf-skewed routes (routed experts only); trace: the reference's measured OLMoE "
                          "RouteTrace (128-token prefill + 31 decode tokens over 16 layers) replayed through "
                          "c1-shaped Q4 layers; qwen: end-to-end greedy decode of a Qwen1.5-MoE-A2.7B-shaped model "
-                         "(synthetic weights) through the host integration, one HIP graph per token")
+                         "(synthetic weights) through the host integration, one HIP graph per token; pack: open, "
+                         "validate and stage a Q4 TargetPack of c2 layers with the library's pack reader")
     ap.add_argument("--tokens", type=int, default=0, help="tokens per call (0: the config's own)")
     ap.add_argument("--rotate-bytes", type=float, default=1.1e9)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -621,6 +622,63 @@ def main_qwen(args, torch, syn, ext) -> int:
         unregister_expert_pack(handle)
 
 
+def main_pack(args, torch, syn, ext) -> int:
+    """The pack reader (f1) on a Q4 TargetPack of four c2-shaped layers
+    written to local disk: open + full validation (both SHA-256s over every
+    byte, per-tensor hashes, payload scans) and staging of each layer to the
+    device, in GB/s of pack bytes. The file is read from the page cache
+    (written just before), so these are the reader's own rates, not the
+    disk's."""
+    import tempfile
+
+    from uma_qmoe_amd.native_backend import stage_experts
+    from uma_qmoe_amd.packfile import TargetPackReader, write_target_pack
+
+    dev = torch.device("cuda:0")
+    layers = 4
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as tmp:
+        path = Path(tmp) / "c2_q4.uqtp"
+        progress(f"pack: writing {layers} c2 layers")
+
+        def tensors():
+            for l in range(layers):
+                built = syn.build_experts(syn.C2, layer=l, device=dev)
+                for name, t in syn.pack_tensors({0: built}):
+                    yield name.replace("layers.0.", f"layers.{l}."), t
+
+        write_target_pack(path, tensors(), model_id="Qwen/Qwen1.5-MoE-A2.7B", model_revision="a" * 40,
+                          model_manifest_sha256="b" * 64, policy_id="bench-q4",
+                          layer_encodings={i: "q4_group128" for i in range(24)}, policy_evidence_sha256="e" * 64)
+        size = path.stat().st_size
+        opens, stages = [], []
+        for rep in range(3):
+            t0 = time.perf_counter()
+            reader = TargetPackReader(path)
+            opens.append(time.perf_counter() - t0)
+            try:
+                t0 = time.perf_counter()
+                for l in range(layers):
+                    staged = stage_experts(reader, l, dev)
+                torch.cuda.synchronize()
+                stages.append(time.perf_counter() - t0)
+                del staged
+            finally:
+                reader.close()
+            progress(f"pack: pass {rep + 1}: open {opens[-1]:.3f} s, stage {stages[-1]:.3f} s")
+    o, st = sorted(opens)[1], sorted(stages)[1]
+    line = {
+        "metric": "pack reader: open + validate and stage to HBM, GB/s of pack bytes",
+        "value": round(size / st / 1e9, 3), "unit": "GB/s (staging)", "n_gpus": 1, "steps": 3, "warmup": 0,
+        "ms_per_step": round(st * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8", "data": "synthetic (c2 Q4 layers written to a pack file on local disk, page cache warm)",
+        "config": {"workload": f"pack: {layers} c2 Q4 layers, {size} bytes", "tokens": 0, "parallelism": "single GPU"},
+        "open_validate_s": round(o, 4), "open_validate_gbps": round(size / o / 1e9, 3),
+        "stage_s": round(st, 4), "host_threads": len(os.sched_getaffinity(0)),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main_trace(args, torch, syn, ext) -> int:
     """Replays the measured routes of the reference's RouteTrace (OLMoE,
     batch 1, 128 prompt tokens, 32 output tokens: one prefill event, 31
@@ -749,6 +807,8 @@ def main() -> int:
         return main_stack(args, torch, syn, ext)
     if args.config == "qwen":
         return main_qwen(args, torch, syn, ext)
+    if args.config == "pack":
+        return main_pack(args, torch, syn, ext)
     if args.config == "trace":
         return main_trace(args, torch, syn, ext)
     if args.multi_kernel:

@@ -49,7 +49,8 @@ enum {
   UQM_ERR_ARGUMENT = 1,  /* shape / pointer / alignment / range error      */
   UQM_ERR_HIP = 2,       /* a HIP runtime call or kernel launch failed       */
   UQM_ERR_DEVICE = 3,    /* current device is not gfx950                     */
-  UQM_ERR_WORKSPACE = 4  /* workspace missing or smaller than required       */
+  UQM_ERR_WORKSPACE = 4, /* workspace missing or smaller than required       */
+  UQM_ERR_PACK = 5       /* pack file unreadable or violating its contract   */
 };
 
 enum { UQM_Q4 = 0, UQM_Q8 = 1, UQM_BF16 = 2 };

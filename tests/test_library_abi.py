@@ -1,5 +1,5 @@
-"""The C-ABI library loads and exports every entry point include/uma_qmoe_hip.h
-declares (no compute calls: this runs without a GPU)."""
+"""The C-ABI library loads and exports every entry point include/*.h declares
+(no compute calls: this runs without a GPU)."""
 
 from __future__ import annotations
 
@@ -9,11 +9,12 @@ from pathlib import Path
 
 from uma_qmoe_amd import _native
 
-HEADER = Path(__file__).resolve().parent.parent / "include" / "uma_qmoe_hip.h"
+INCLUDE = Path(__file__).resolve().parent.parent / "include"
+HEADER = INCLUDE / "uma_qmoe_hip.h"
 
 
 def declared_functions() -> list[str]:
-    text = HEADER.read_text()
+    text = "".join(h.read_text() for h in sorted(INCLUDE.glob("*.h")))
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(uqm_[a-z0-9_]+)\s*\(", text)))
 
@@ -46,8 +47,8 @@ def test_struct_layouts_match_header():
     assert ctypes.sizeof(_native.LayerWeights) == ctypes.sizeof(_native.ExpertWeights) + 8 + 8 + 4 + 4 + 8 + 4 * 8
 
 
-def header_enum_values() -> dict[str, int]:
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+def header_enum_values(header: Path = HEADER) -> dict[str, int]:
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
     values = {}
     for body in re.findall(r"enum\s*\{(.*?)\}", text, flags=re.S):
         for name, value in re.findall(r"\b(UQM_[A-Z0-9_]+)\s*=\s*(\d+)", body):
@@ -58,8 +59,16 @@ def header_enum_values() -> dict[str, int]:
 def test_python_constants_match_header_enums():
     values = header_enum_values()
     for name in ("UQM_Q4", "UQM_Q8", "UQM_BF16", "UQM_OPT_FUSED_DECODE",
-                 "UQM_OPT_MFMA_MIN_TOKENS", "UQM_OPT_OVERLAP_SHARED", "UQM_OPT_STREAM_MAX_ROUTES"):
+                 "UQM_OPT_MFMA_MIN_TOKENS", "UQM_OPT_OVERLAP_SHARED", "UQM_OPT_STREAM_MAX_ROUTES", "UQM_ERR_PACK"):
         assert values[name] == getattr(_native, name), name
+    pack_enums = header_enum_values(INCLUDE / "uma_qmoe_pack.h")
+    assert (pack_enums["UQM_PACK_EXPERT"], pack_enums["UQM_PACK_TARGET"]) == (0, 1)
+    assert (pack_enums["UQM_PROJ_GATE"], pack_enums["UQM_PROJ_UP"], pack_enums["UQM_PROJ_DOWN"]) == (0, 1, 2)
+
+
+def test_pack_tensor_struct_layout():
+    # uqm_pack_tensor: 2 pointers, 2 x uint64, int64, int64[4], 4 x int32
+    assert ctypes.sizeof(_native.PackTensor) == 2 * 8 + 2 * 8 + 8 + 4 * 8 + 4 * 4
 
 
 def test_set_option_is_host_only_and_validates():

@@ -1,4 +1,5 @@
-"""ctypes binding of libuma_qmoe_hip.so (the C ABI in include/uma_qmoe_hip.h).
+"""ctypes binding of libuma_qmoe_hip.so (the C ABI in include/uma_qmoe_hip.h and
+include/uma_qmoe_pack.h).
 
 Loading never falls back to anything: if the library is missing or was built
 for another ABI, :func:`library` raises. Build it with
@@ -27,7 +28,8 @@ UQM_OPT_STREAM_MAX_ROUTES = 5
 
 ENCODING_IDS = {"q4_group128": UQM_Q4, "q8_group128": UQM_Q8, "bf16_le": UQM_BF16}
 
-ERROR_NAMES = {1: "argument", 2: "hip", 3: "device", 4: "workspace"}
+UQM_ERR_PACK = 5
+ERROR_NAMES = {1: "argument", 2: "hip", 3: "device", 4: "workspace", UQM_ERR_PACK: "pack"}
 
 _LOCK = threading.Lock()
 _LIB = None
@@ -72,6 +74,27 @@ class LayerWeights(ctypes.Structure):
     ]
 
 
+class PackTensor(ctypes.Structure):
+    """uqm_pack_tensor."""
+
+    _fields_ = [
+        ("data", _vp),
+        ("data_bytes", ctypes.c_uint64),
+        ("scales", _vp),
+        ("scale_bytes", ctypes.c_uint64),
+        ("element_count", _i64),
+        ("shape", _i64 * 4),
+        ("ndim", _i32),
+        ("encoding", _i32),
+        ("group_size", _i32),
+        ("reserved", _i32),
+    ]
+
+
+_cp = ctypes.c_char_p
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+_i32p = ctypes.POINTER(_i32)
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "uqm_abi_version": (ctypes.c_int, ()),
@@ -105,6 +128,13 @@ SIGNATURES = {
     "uqm_rmsnorm": (ctypes.c_int, (_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _vp)),
     "uqm_set_option": (ctypes.c_int, (ctypes.c_int, _i64)),
     "uqm_workspace_status": (ctypes.c_int, (_vp, ctypes.c_size_t, _vp)),
+    "uqm_pack_open": (ctypes.c_int, (_cp, _i32, _cp, _cp, _cp, _cp, ctypes.POINTER(_vp))),
+    "uqm_pack_close": (ctypes.c_int, (_vp,)),
+    "uqm_pack_info": (ctypes.c_int, (_vp, _i32p, _u64p, _u64p, _i32p)),
+    "uqm_pack_header": (ctypes.c_int, (_vp, ctypes.POINTER(_cp), ctypes.POINTER(ctypes.c_size_t))),
+    "uqm_pack_lookup": (ctypes.c_int, (_vp, _cp, ctypes.POINTER(PackTensor))),
+    "uqm_pack_layer_encoding": (ctypes.c_int, (_vp, _i64, _i32p)),
+    "uqm_pack_stage_projection": (ctypes.c_int, (_vp, _i64, _i32, _i64, _vp, _vp, _vp)),
 }
 
 

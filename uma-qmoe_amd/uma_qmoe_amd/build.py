@@ -1,7 +1,8 @@
 """Builds libuma_qmoe_hip.so for gfx950 with hipcc (in-tree, no JIT cache).
 
-Each ``csrc/*.hip`` translation unit is compiled in parallel to an object
-under ``_build/`` and linked into ``uma-qmoe_amd/lib/libuma_qmoe_hip.so``;
+Each ``csrc/*.hip`` translation unit (hipcc) and each host-only
+``csrc/*.cpp`` one (g++) is compiled in parallel to an object under
+``_build/`` and linked into ``uma-qmoe_amd/lib/libuma_qmoe_hip.so``;
 ``csrc/timeline/fused_timeline.hip`` becomes the program
 ``uma-qmoe_amd/lib/fused_timeline``.
 Run as ``python -m uma_qmoe_amd.build`` with ``uma-qmoe_amd`` on sys.path.
@@ -38,16 +39,26 @@ COMMON_FLAGS = [
 ]
 
 
+CXX = os.environ.get("CXX", "g++")
+# Host-only translation units (the pack reader): plain C++ against the HIP
+# runtime API, linked with OpenSSL's libcrypto for SHA-256.
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
+LINK_LIBS = ["-lcrypto", "-lpthread"]
+
+
 def sources() -> list[Path]:
-    return sorted(CSRC.glob("*.hip"))
+    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    if src.suffix == ".cpp":
+        cmd = [CXX, *HOST_FLAGS, "-c", str(src), "-o", str(obj)]
+    else:
+        cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
+        raise RuntimeError(f"compilation failed for {src.name}:\n{proc.stderr}")
     return obj
 
 
@@ -81,7 +92,7 @@ def build(verbose: bool = False) -> Path:
         objs = list(pool.map(_compile, srcs))
         timeline.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), *LINK_LIBS, "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")

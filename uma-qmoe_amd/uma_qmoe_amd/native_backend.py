@@ -495,9 +495,11 @@ def stage_experts(reader: Any, layer_index: int, device: Any, num_experts: int |
 
     The staged layout is the reference's (_host_projection / _device_layer,
     src/uma_qmoe/native_backend.py:374-455, 769-842): projection by
-    projection, experts 0..E-1 concatenated, every expert of one shape. The
-    bytes go from the reader's views into a pinned buffer and from there to
-    the device in one copy per tensor kind, nothing is expanded.
+    projection, experts 0..E-1 concatenated, every expert of one shape,
+    nothing expanded. A pack file opened by the library's reader is staged by
+    the library itself (``uqm_pack_stage_projection``: straight from the
+    mapping through pinned buffers to the device); other readers' views are
+    gathered here into one pinned buffer and copied once per tensor kind.
     """
     import numpy as np
     import torch
@@ -514,8 +516,32 @@ def stage_experts(reader: Any, layer_index: int, device: Any, num_experts: int |
     header = getattr(reader, "header", None)
     quant = header.get("quantization") if isinstance(header, dict) else None
     group = int(quant.get("group_size", 128)) if isinstance(quant, dict) else 128
+    native = dev.type == "cuda" and callable(getattr(reader, "stage_projection", None))
     with stg.lock:
         for proj in PROJECTIONS:
+            if native:
+                name = EXPERT_NAME.format(layer=layer_index, expert=0, proj=proj)
+                data, scales, meta = reader.tensor_views(name)
+                db, sb = len(data), len(scales)
+                _release(data, scales)
+                if meta.get("encoding", encoding) != encoding:
+                    raise RuntimeError(f"tensor {name!r} is {meta.get('encoding')}, layer {layer_index} is {encoding}")
+                shape = tuple(int(v) for v in meta["shape"])
+                if len(shape) != 2:
+                    raise RuntimeError(f"expert tensor {name!r} is not a matrix")
+                shapes[proj] = shape
+                if meta.get("group_size"):
+                    group = int(meta["group_size"])
+                s0 = -(-E * db // 256) * 256  # scales start 256-byte aligned
+                staged = torch.empty(s0 + E * sb, dtype=torch.uint8, device=dev)
+                reader.stage_projection(layer_index, proj, E, staged.data_ptr(),
+                                        staged.data_ptr() + s0 if sb else 0,
+                                        torch.cuda.current_stream(dev).cuda_stream)
+                rows, cols = shape
+                data = staged[:E * db].view({"u1": torch.uint8, "i1": torch.int8,
+                                             "<u2": torch.bfloat16}[_NP_DTYPE[encoding]]).view(E, rows, -1)
+                out[proj] = (data, staged[s0:].view(torch.float32).view(E, -1) if sb else None)
+                continue
             views = []
             try:
                 for e in range(E):

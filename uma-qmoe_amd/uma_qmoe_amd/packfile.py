@@ -20,31 +20,30 @@ model identity is the SHA-256 of the canonical JSON of {model_id,
 model_revision, model_manifest_sha256}; a TargetPack's policy identity is the
 SHA-256 of {policy_id, layer_encodings, policy_evidence_sha256}.
 
-``PackReader`` maps the file once (the custom operator requires exactly one
-mapping per pack) and validates it completely before use: prefix, both
-hashes, canonical JSON, identities, the layout of every tensor, zero padding,
-per-tensor hashes and the payload semantics (no reserved Q4 code, zero Q4
-tail nibble, finite positive scales), with the byte checks run by numpy over
-the mapping rather than per element in Python. Tensor views are zero-copy
-slices of the mapping; the HIP backend stages a layer's experts from them
-with one pinned DMA per projection.
+``PackReader`` is the library's C++ reader (csrc/uqm_pack.cpp): it maps the
+file once (the custom operator requires exactly one mapping per pack) and
+validates it completely before use: prefix, both hashes, canonical JSON,
+identities, the layout of every tensor, zero padding, per-tensor hashes and
+the payload semantics (no reserved Q4 code, zero Q4 tail nibble, finite
+positive scales), on worker threads. Tensor views are zero-copy slices of the
+mapping; the HIP backend stages a layer's experts straight from the mapping
+through pinned buffers to the device (``stage_projection``).
 """
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass, field
 import hashlib
 import json
-import math
-import mmap
 import os
 from pathlib import Path
 import re
 import struct
 import tempfile
 from typing import Any, Iterable, Iterator, Mapping
+import weakref
 
-import numpy as np
 
 from .formats import (
     ENCODINGS,
@@ -308,196 +307,100 @@ def write_target_pack(destination: str | Path, tensors: Iterable[tuple[str, Any]
 
 
 # ------------------------------------------------------------------ reader --
+_ENCODING_NAMES = {0: "q4_group128", 1: "q8_group128", 2: "bf16_le"}  # UQM_Q4 / UQM_Q8 / UQM_BF16
+_PACK_KINDS = {0: EXPERT_PACK, 1: TARGET_PACK}  # UQM_PACK_EXPERT / UQM_PACK_TARGET
+_PROJECTION_IDS = {"gate_proj": 0, "up_proj": 1, "down_proj": 2}
+
+
 class PackReader:
-    """One read-only descriptor and one mmap of a validated pack file."""
+    """A validated pack file, read by the library's C++ reader
+    (csrc/uqm_pack.cpp, ``uqm_pack_open``): one read-only mapping, every
+    check of the format made before the constructor returns, and the first
+    violation raised as ``ContractError`` with the reference reader's
+    message. ``tensor_views`` are zero-copy views of the mapping; after
+    ``close()`` the mapping lives on until the last view handed out is
+    released."""
 
     kind: _Kind | None = None  # set by the kind-specific subclasses
 
     def __init__(self, path: str | Path, *, expected_model_id: str | None = None,
                  expected_model_revision: str | None = None, expected_model_manifest_sha256: str | None = None,
                  expected_policy_id: str | None = None) -> None:
+        from . import _native
+
         self.path = Path(path)
-        self._file = None
-        self._map = None
-        label = self.kind.label if self.kind else "pack"
-        try:
-            self._file = self.path.open("rb")
-            self._map = mmap.mmap(self._file.fileno(), 0, access=mmap.ACCESS_READ)
-        except (OSError, ValueError) as exc:
-            self.close()
-            raise ContractError(f"cannot map {label} {self.path}: {exc}") from exc
+        self._lib = _native.library()
+        self._handle = None
+        self._closed = False
+        self._live_views = 0
+        want_kind = -1 if self.kind is None else (0 if self.kind is EXPERT_PACK else 1)
+
+        def c(v: str | None):
+            return None if v is None else str(v).encode("utf-8")
+
+        handle = ctypes.c_void_p()
+        rc = self._lib.uqm_pack_open(os.fsencode(self.path), want_kind, c(expected_model_id),
+                                     c(expected_model_revision), c(expected_model_manifest_sha256),
+                                     c(expected_policy_id), ctypes.byref(handle))
+        self._check(rc, "uqm_pack_open")
+        self._handle = handle
         self.mapping_count = 1
-        try:
-            self._validate(expected_model_id, expected_model_revision, expected_model_manifest_sha256,
-                           expected_policy_id)
-        except BaseException:
-            self.close()
-            raise
+        kind, poff, plen, group = ctypes.c_int32(), ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_int32()
+        self._check(self._lib.uqm_pack_info(handle, ctypes.byref(kind), ctypes.byref(poff), ctypes.byref(plen),
+                                            ctypes.byref(group)), "uqm_pack_info")
+        self.kind = _PACK_KINDS[kind.value]
+        self.payload_offset, self.payload_length, self.group_size = poff.value, plen.value, group.value
+        text, length = ctypes.c_char_p(), ctypes.c_size_t()
+        self._check(self._lib.uqm_pack_header(handle, ctypes.byref(text), ctypes.byref(length)), "uqm_pack_header")
+        self.header = json.loads(ctypes.string_at(text, length.value))
         self._index = {t["name"]: t for t in self.header["tensors"]}
 
-    # -- validation ----------------------------------------------------------
-    def _bytes(self, start: int, stop: int) -> np.ndarray:
-        return np.frombuffer(self._map, dtype=np.uint8, count=stop - start, offset=start)
+    def _check(self, rc: int, what: str) -> None:
+        from . import _native
 
-    def _zero(self, start: int, stop: int, what: str) -> None:
-        if stop > start and self._bytes(start, stop).any():
-            raise ContractError(f"{self.kind.label} {what} padding must be zero")
-
-    def _validate(self, want_id, want_revision, want_manifest, want_policy) -> None:
-        if len(self._map) < PREFIX.size:
-            raise ContractError("pack is shorter than its fixed prefix")
-        magic, version, hlen, poff, plen, hsha, psha = PREFIX.unpack_from(self._map)
-        kind = _KINDS.get(magic)
-        if kind is None or version != VERSION or (self.kind is not None and kind is not self.kind):
-            raise ContractError(f"{(self.kind or kind or EXPERT_PACK).label} magic/version mismatch")
-        self.kind = kind
-        L = kind.label
-        if poff % HEADER_ALIGNMENT or poff < PREFIX.size + hlen:
-            raise ContractError(f"{L} payload offset/alignment is invalid")
-        if poff + plen != len(self._map):
-            raise ContractError(f"{L} payload length does not match file size")
-        hb = bytes(self._map[PREFIX.size:PREFIX.size + hlen])
-        if hashlib.sha256(hb).digest() != hsha:
-            raise ContractError(f"{L} header hash mismatch")
-        self._zero(PREFIX.size + hlen, poff, "header")
-        view = memoryview(self._map)[poff:poff + plen]
-        try:
-            if hashlib.sha256(view).digest() != psha:
-                raise ContractError(f"{L} payload hash mismatch")
-        finally:
-            view.release()
-        try:
-            header = json.loads(hb)
-        except (UnicodeDecodeError, json.JSONDecodeError) as exc:
-            raise ContractError(f"{L} header is not canonical JSON") from exc
-        if not isinstance(header, dict) or canonical_json(header) != hb:
-            raise ContractError(f"{L} header JSON is not canonical")
-        fmt = "canonical_q4_symmetric_grouped" if kind is EXPERT_PACK else "mixed_precision_target_pack"
-        if header.get("schema_version") != VERSION or header.get("format") != fmt:
-            raise ContractError(f"{L} header schema is unsupported")
-        model = header.get("model")
-        tensors = header.get("tensors")
-        if not isinstance(model, dict) or not isinstance(tensors, list):
-            raise ContractError(f"{L} header is incomplete")
-        if model.get("model_identity_sha256") != model_identity(model.get("model_id", ""),
-                                                                model.get("model_revision", ""),
-                                                                model.get("model_manifest_sha256", "")):
-            raise ContractError(f"{L} model identity hash mismatch")
-        policy = header.get("policy") if kind is TARGET_PACK else None
-        for want, seen, what in ((want_id, model.get("model_id"), "model id"),
-                                 (want_revision, model.get("model_revision"), "model revision"),
-                                 (want_manifest, model.get("model_manifest_sha256"), "model manifest"),
-                                 (want_policy, (policy or {}).get("policy_id") if kind is TARGET_PACK else want_policy,
-                                  "policy id")):
-            if want is not None and want != seen:
-                raise ContractError(f"{L} {what} mismatch")
-        if kind is EXPERT_PACK:
-            q = header.get("quantization")
-            group = q.get("group_size") if isinstance(q, dict) else None
-            if q != {**Q4_CONTRACT, "group_size": group} or isinstance(group, bool) or not isinstance(group, int) \
-                    or group <= 0:
-                raise ContractError("ExpertPack quantization contract mismatch")
-            layer_enc: dict[int, str] = {}
-        else:
-            model_name, layers, experts = fixed_model_dims(model.get("model_id"))
-            if not isinstance(policy, dict) or not isinstance(policy.get("layer_encodings"), dict):
-                raise ContractError("TargetPack layer policy is invalid")
-            try:
-                layer_enc = {int(i): e for i, e in policy["layer_encodings"].items()}
-            except (TypeError, ValueError) as exc:
-                raise ContractError("TargetPack layer policy is invalid") from exc
-            if policy != policy_block(policy.get("policy_id", ""), layer_enc, policy.get("policy_evidence_sha256", ""),
-                                      layers, model_name):
-                raise ContractError("TargetPack policy identity hash mismatch")
-            if header.get("encodings") != TARGET_ENCODINGS:
-                raise ContractError("TargetPack encoding contract mismatch")
-            group = GROUP_SIZE
-        alignment = _check_alignment(header.get("tensor_alignment_bytes"))
-        if not tensors or header.get("tensor_count") != len(tensors):
-            raise ContractError(f"{L} tensor count is inconsistent")
-        counts = {e: 0 for e in sorted(ENCODINGS)}
-        seen: set[str] = set()
-        end_prev = 0
-        for t in tensors:
-            end_prev = self._validate_tensor(t, kind, group, alignment, layer_enc, seen, end_prev, poff, plen,
-                                             counts, model.get("model_id"))
-        if end_prev != plen:
-            raise ContractError(f"{L} payload has unclaimed trailing bytes")
-        if kind is TARGET_PACK and header.get("encoding_tensor_counts") != counts:
-            raise ContractError("TargetPack encoding tensor counts are inconsistent")
-        self.header, self.payload_offset, self.payload_length = header, poff, plen
-        self.group_size = group
-
-    def _validate_tensor(self, t, kind, group, alignment, layer_enc, seen, end_prev, poff, plen, counts, model_id):
-        L = kind.label
-        if not isinstance(t, dict):
-            raise ContractError(f"{L} tensor header must be an object")
-        name = t.get("name")
-        if kind is EXPERT_PACK:
-            if not isinstance(name, str) or not _SAFE_NAME.fullmatch(name) or name in seen:
-                raise ContractError("ExpertPack tensor names must be unique and safe")
-            enc = Q4.name
-        else:
-            m = _EXPERT_NAME.fullmatch(name) if isinstance(name, str) else None
-            if m is None or name in seen:
-                raise ContractError("TargetPack tensor names must be unique fixed expert tensors")
-            _, layers, experts = fixed_model_dims(model_id)
-            layer, expert = int(m.group(1)), int(m.group(2))
-            enc = t.get("encoding")
-            if (layer >= layers or expert >= experts or t.get("layer_index") != layer
-                    or t.get("expert_index") != expert or t.get("projection") != m.group(3)
-                    or enc != layer_enc.get(layer)):
-                raise ContractError(f"TargetPack tensor {name!r} policy identity is invalid")
-        seen.add(name)
-        shape = t.get("shape")
-        if not isinstance(shape, list) or not shape or any(
-                isinstance(d, bool) or not isinstance(d, int) or d <= 0 for d in shape):
-            raise ContractError(f"{L} tensor {name!r} has invalid shape")
-        n = math.prod(shape)
-        e = ENCODINGS[enc]
-        g = group if e.grouped else None
-        start, nbytes = t.get(f"{kind.data_field}_offset"), t.get(f"{kind.data_field}_bytes")
-        scale_at, sbytes, end = t.get("scale_offset"), t.get("scale_bytes"), t.get("storage_end_offset")
-        ints = all(isinstance(v, int) and not isinstance(v, bool) for v in (start, nbytes, scale_at, sbytes, end))
-        if (not ints or t.get("element_count") != n or nbytes != e.data_bytes(n)
-                or sbytes != e.scale_bytes(n, group) or t.get("group_count") != (-(-n // group) if e.grouped else 0)
-                or (kind is TARGET_PACK and t.get("group_size") != g)
-                or start % alignment or start < end_prev or scale_at != _align(start + nbytes, 4)
-                or end != _align(scale_at + sbytes, alignment) or end > plen):
-            raise ContractError(f"{L} tensor {name!r} layout is invalid")
-        if t.get("effective_bits_per_weight") != (end - start) * 8 / n:
-            raise ContractError(f"{L} tensor {name!r} effective bpw is invalid")
-        self._zero(poff + end_prev, poff + start, f"tensor {name!r} leading")
-        self._zero(poff + start + nbytes, poff + scale_at, f"tensor {name!r} data-to-scale")
-        self._zero(poff + scale_at + sbytes, poff + end, f"tensor {name!r} trailing")
-        data = self._bytes(poff + start, poff + start + nbytes)
-        scales = self._bytes(poff + scale_at, poff + scale_at + sbytes)
-        h = hashlib.sha256(data)
-        h.update(scales)
-        if h.hexdigest() != t.get("tensor_payload_sha256"):
-            raise ContractError(f"{L} tensor {name!r} hash mismatch")
-        check_payload(enc, data, scales, n, group, f"{L} tensor {name!r}")
-        counts[enc] += 1
-        return end
+        if rc == _native.UQM_ERR_PACK:
+            raise ContractError(self._lib.uqm_last_error().decode("utf-8", "replace"))
+        _native.check(rc, what)
 
     # -- access ----------------------------------------------------------------
     def _entry(self, name: str) -> dict[str, Any]:
-        if self._map is None:
+        if self._closed:
             raise ContractError(f"{self.kind.label} is closed")
         try:
             return self._index[name]
         except KeyError:
             raise ContractError(f"{self.kind.label} has no tensor {name!r}") from None
 
+    def _lookup(self, name: str):
+        from . import _native
+
+        self._entry(name)
+        info = _native.PackTensor()
+        self._check(self._lib.uqm_pack_lookup(self._handle, name.encode("utf-8"), ctypes.byref(info)),
+                    "uqm_pack_lookup")
+        return info
+
+    def _view(self, address: int, nbytes: int) -> memoryview:
+
+        if nbytes == 0 or not address:
+            return memoryview(b"")
+        array = (ctypes.c_ubyte * nbytes).from_address(address)
+        self._live_views += 1
+        weakref.finalize(array, self._view_released)
+        return memoryview(array).cast("B")
+
+    def _view_released(self) -> None:
+        self._live_views -= 1
+        if self._closed and self._live_views == 0:
+            self._release()
+
     def tensor_views(self, name: str) -> tuple[memoryview, memoryview, Mapping[str, Any]]:
         """Zero-copy (data, scales, header entry) of one tensor; the entry
         carries ``shape`` and ``encoding`` (and ``group_size``)."""
         t = self._entry(name)
-        d0 = self.payload_offset + t[f"{self.kind.data_field}_offset"]
-        s0 = self.payload_offset + t["scale_offset"]
+        info = self._lookup(name)
         meta = t if self.kind is TARGET_PACK else {**t, "encoding": Q4.name, "group_size": self.group_size}
-        mv = memoryview(self._map)
-        return (mv[d0:d0 + t[f"{self.kind.data_field}_bytes"]], mv[s0:s0 + t["scale_bytes"]], meta)
+        return (self._view(info.data or 0, info.data_bytes), self._view(info.scales or 0, info.scale_bytes), meta)
 
     def tensor(self, name: str) -> TargetTensor:
         data, scales, meta = self.tensor_views(name)
@@ -515,29 +418,44 @@ class PackReader:
         return Q4Tensor(t.shape, int(t.group_size), t.data, t.scales)
 
     def layer_encoding(self, layer_index: int) -> str:
-        if self.kind is EXPERT_PACK:
-            return Q4.name
-        _, layers, _ = fixed_model_dims(self.header["model"]["model_id"])
-        if not 0 <= layer_index < layers:
-            raise ContractError(f"TargetPack layer index must be in [0, {layers - 1}]")
-        return self.header["policy"]["layer_encodings"][str(layer_index)]
+        if self._closed:
+            raise ContractError(f"{self.kind.label} is closed")
+        enc = ctypes.c_int32()
+        self._check(self._lib.uqm_pack_layer_encoding(self._handle, int(layer_index), ctypes.byref(enc)),
+                    "uqm_pack_layer_encoding")
+        return _ENCODING_NAMES[enc.value]
 
     def names(self) -> list[str]:
         return list(self._index)
 
+    def stage_projection(self, layer_index: int, projection: str, num_experts: int, data_dst: int,
+                         scales_dst: int, stream: int) -> None:
+        """Copies ``projection`` of experts 0..num_experts-1 of one layer to
+        the device addresses given (data expert-major, scales expert-major)
+        through the reader's pinned buffers; returns when the copies are done."""
+        if self._closed:
+            raise ContractError(f"{self.kind.label} is closed")
+        self._check(self._lib.uqm_pack_stage_projection(self._handle, int(layer_index), _PROJECTION_IDS[projection],
+                                                        int(num_experts), data_dst, scales_dst or None, stream),
+                    "uqm_pack_stage_projection")
+
+    def _release(self) -> None:
+        if self._handle is not None:
+            self._lib.uqm_pack_close(self._handle)
+            self._handle = None
+
     def close(self) -> None:
-        """Unmaps the file; if views handed out (or held by an exception's
-        traceback) still export the mapping, it is unmapped when the last of
-        them is released."""
-        if self._map is not None:
-            try:
-                self._map.close()
-            except BufferError:
-                pass
-            self._map = None
-        if self._file is not None:
-            self._file.close()
-            self._file = None
+        """Closes the pack; the mapping is released now, or when the last
+        view handed out is released."""
+        if self._closed:
+            return
+        self._closed = True
+        if self._live_views == 0:
+            self._release()
+
+    def __del__(self) -> None:
+        if getattr(self, "_handle", None) is not None and getattr(self, "_live_views", 0) == 0:
+            self._release()
 
     def __enter__(self):
         return self
@@ -573,8 +491,9 @@ def open_pack(path: str | Path, **expected: Any) -> PackReader:
 def inspect_pack(path: str | Path) -> dict[str, Any]:
     """Verified manifest record of a pack file (src/uma_qmoe/expert_pack.py:559-582)."""
     source = Path(path)
+    with source.open("rb") as f:
+        prefix = PREFIX.unpack(f.read(PREFIX.size))
     with open_pack(source) as reader:
-        prefix = PREFIX.unpack_from(reader._map)
         header = reader.header
         kind = reader.kind
         poff, plen = reader.payload_offset, reader.payload_length
