@@ -1,0 +1,135 @@
+// HBM read rate of the weight-streaming patterns the grouped GEMM can use.
+//
+// A 149 MB matrix of 1 KB rows (a batch-32 call's routed gate/up bytes),
+// eight copies rotated (1.2 GB, beyond the 256 MB infinity cache), read by a
+// persistent grid of 256 workgroups (one per CU), each taking blocks of 128
+// rows round robin and reading every byte once in 16 steps of 8 KB:
+//   pattern 0: every 1 KB load covers 16 rows x 64 B at one K offset, steps
+//              walk K (the MFMA lane layout, the grouped GEMM's order);
+//   pattern 1: every 1 KB load covers one row's 1 KB.
+// Two ways of reading:
+//   dma: global_load_lds (16 B per lane) into an LDS ring of 6 steps, issued
+//        by one wave per workgroup (2 and 4 waves give the same rate);
+//   ldg: plain 16-byte loads into registers by 8 waves per workgroup, 4 steps
+//        in flight per wave.
+// Prints GB/s for each (median of 24 launches after 3 warm-up launches).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBlocks = 1166;  // x 128 rows x 1 KB
+constexpr size_t kBytes = static_cast<size_t>(kBlocks) * 128 * 1024;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Load i (0..7) of step s of a 128-row block.
+__device__ __forceinline__ const uint8_t* at(const uint8_t* b, int pattern, int s, int i, int lane) {
+  if (pattern == 0) return b + (i * 16 + (lane & 15)) * 1024 + s * 64 + (lane >> 4) * 16;
+  return b + (s * 8 + i) * 1024 + lane * 16;
+}
+
+constexpr int kDepth = 6;
+
+__global__ __launch_bounds__(64) void dma_read(const uint8_t* w, int pattern, int* sink) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int lane = threadIdx.x;
+  const uint32_t base =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)lds));
+  int issued = 0;
+  for (int blk = blockIdx.x; blk < kBlocks; blk += gridDim.x) {
+    const uint8_t* b = w + static_cast<int64_t>(blk) * 128 * 1024;
+    for (int s = 0; s < 16; ++s) {
+      const uint32_t buf = __builtin_amdgcn_readfirstlane(base + (issued % kDepth) * 8192);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        __builtin_amdgcn_global_load_lds(at(b, pattern, s, i, lane),
+                                         reinterpret_cast<lds_void_t*>(static_cast<uintptr_t>(buf + i * 1024)), 16, 0, 0);
+      ++issued;
+      if (issued >= kDepth) wait_vmcnt<(kDepth - 1) * 8>();  // the buffer about to be reused has landed
+    }
+  }
+  wait_vmcnt<0>();
+  if (lane == 0 && issued < 0) sink[0] = lds[0];
+}
+
+constexpr int kWaves = 8, kAhead = 4;
+
+__global__ __launch_bounds__(64 * kWaves) void ldg_read(const uint8_t* w, int pattern, int* sink) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nb = (kBlocks - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+  const int total = nb * 16;  // steps of this workgroup; each wave loads one of the 8 loads per step
+  auto src = [&](int g) {
+    const int blk = static_cast<int>(blockIdx.x) + (g / 16) * static_cast<int>(gridDim.x);
+    return reinterpret_cast<const u32x4*>(at(w + static_cast<int64_t>(blk) * 128 * 1024, pattern, g % 16, wave, lane));
+  };
+  uint32_t acc = 0;
+  int g = 0;
+  for (; g + kAhead <= total; g += kAhead) {
+    u32x4 v[kAhead];
+#pragma unroll
+    for (int d = 0; d < kAhead; ++d) v[d] = __builtin_nontemporal_load(src(g + d));
+#pragma unroll
+    for (int d = 0; d < kAhead; ++d) acc ^= v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+  }
+  for (; g < total; ++g) {
+    const u32x4 v = __builtin_nontemporal_load(src(g));
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == 0x9E3779B9u) sink[0] = static_cast<int>(acc);  // keeps the loads
+}
+
+float gbps(bool dma, int pattern, const uint8_t* w, int* sink) {
+  hipEvent_t ev[27];
+  for (auto& e : ev)
+    if (hipEventCreate(&e) != hipSuccess) return -1.0f;
+  for (int r = 0; r < 27; ++r) {
+    if (r >= 3 && hipEventRecord(ev[r - 3 + 0]) != hipSuccess) return -1.0f;
+    const uint8_t* src = w + (r % 8) * kBytes;
+    if (dma)
+      hipLaunchKernelGGL(dma_read, dim3(256), dim3(64), kDepth * 8192, 0, src, pattern, sink);
+    else
+      hipLaunchKernelGGL(ldg_read, dim3(256), dim3(64 * kWaves), 0, 0, src, pattern, sink);
+  }
+  if (hipEventRecord(ev[24]) != hipSuccess || hipEventSynchronize(ev[24]) != hipSuccess) return -1.0f;
+  // per-launch times from consecutive events
+  float t[24];
+  for (int k = 0; k < 24; ++k) {
+    if (hipEventElapsedTime(&t[k], ev[k], ev[k + 1]) != hipSuccess) return -1.0f;
+  }
+  for (int a = 0; a < 24; ++a)
+    for (int b = a + 1; b < 24; ++b)
+      if (t[b] < t[a]) {
+        const float x = t[a];
+        t[a] = t[b];
+        t[b] = x;
+      }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  return static_cast<float>(kBytes / (t[12] * 1e-3) / 1e9);
+}
+
+}  // namespace
+
+int main() {
+  uint8_t* w = nullptr;
+  int* sink = nullptr;
+  if (hipMalloc(&w, 8 * kBytes) != hipSuccess || hipMalloc(&sink, 64) != hipSuccess) {
+    fprintf(stderr, "allocation failed\n");
+    return 1;
+  }
+  if (hipMemset(w, 1, 8 * kBytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) return 1;
+  const float d0 = gbps(true, 0, w, sink), d1 = gbps(true, 1, w, sink);
+  const float l0 = gbps(false, 0, w, sink), l1 = gbps(false, 1, w, sink);
+  printf("dma (LDS DMA, 1 wave, 6 steps ahead): 16 rows x 64 B %.0f GB/s, 1 KB rows %.0f GB/s\n", d0, d1);
+  printf("ldg (registers, 8 waves, 4 ahead):    16 rows x 64 B %.0f GB/s, 1 KB rows %.0f GB/s\n", l0, l1);
+  (void)hipFree(w);
+  (void)hipFree(sink);
+  return d0 > 0 && d1 > 0 && l0 > 0 && l1 > 0 ? 0 : 1;
+}

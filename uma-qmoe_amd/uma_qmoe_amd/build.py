@@ -4,7 +4,8 @@ Each ``csrc/*.hip`` translation unit (hipcc) and each host-only
 ``csrc/*.cpp`` one (g++) is compiled in parallel to an object under
 ``_build/`` and linked into ``uma-qmoe_amd/lib/libuma_qmoe_hip.so``;
 ``csrc/timeline/fused_timeline.hip`` becomes the program
-``uma-qmoe_amd/lib/fused_timeline``.
+``uma-qmoe_amd/lib/fused_timeline`` and each ``csrc/probes/NAME.hip`` the
+measurement program ``uma-qmoe_amd/lib/NAME``.
 Run as ``python -m uma_qmoe_amd.build`` with ``uma-qmoe_amd`` on sys.path.
 """
 
@@ -78,6 +79,21 @@ def _compile_timeline() -> Path:
     return TIMELINE_PATH
 
 
+PROBES = CSRC / "probes"
+
+
+def _compile_probe(src: Path) -> Path:
+    """A stand-alone measurement program (csrc/probes/NAME.hip -> lib/NAME)."""
+    out = LIB_DIR / src.stem
+    tmp = out.with_suffix(".tmp")
+    cmd = [HIPCC, *[f for f in COMMON_FLAGS if f != "-fPIC"], str(src), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every HIP source, link the shared library and build the
     timeline program. Always rebuilds."""
@@ -88,9 +104,10 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     jobs = min(len(srcs) + 1, max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        timeline = pool.submit(_compile_timeline)
+        extras = [pool.submit(_compile_timeline)] + [pool.submit(_compile_probe, p) for p in sorted(PROBES.glob("*.hip"))]
         objs = list(pool.map(_compile, srcs))
-        timeline.result()
+        for e in extras:
+            e.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), *LINK_LIBS, "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
