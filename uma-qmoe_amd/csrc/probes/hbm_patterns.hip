@@ -12,6 +12,8 @@
 //        by one wave per workgroup (2 and 4 waves give the same rate);
 //   ldg: plain 16-byte loads into registers by 8 waves per workgroup, 4 steps
 //        in flight per wave.
+// Then the plain-load ceiling for 1 KB rows with 8 or 16 waves per workgroup
+// and 4 or 8 loads in flight per wave.
 // Prints GB/s for each (median of 24 launches after 3 warm-up launches).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -60,15 +62,18 @@ __global__ __launch_bounds__(64) void dma_read(const uint8_t* w, int pattern, in
   if (lane == 0 && issued < 0) sink[0] = lds[0];
 }
 
-constexpr int kWaves = 8, kAhead = 4;
-
+template <int kWaves, int kAhead>
 __global__ __launch_bounds__(64 * kWaves) void ldg_read(const uint8_t* w, int pattern, int* sink) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nb = (kBlocks - static_cast<int>(blockIdx.x) + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
-  const int total = nb * 16;  // steps of this workgroup; each wave loads one of the 8 loads per step
+  // loads of this workgroup: 8 per step, 16 steps per block; wave w takes
+  // loads w, w + kWaves, ... (each load is one (step, i) of the block walk)
+  const int total = nb * 128 / kWaves;
   auto src = [&](int g) {
-    const int blk = static_cast<int>(blockIdx.x) + (g / 16) * static_cast<int>(gridDim.x);
-    return reinterpret_cast<const u32x4*>(at(w + static_cast<int64_t>(blk) * 128 * 1024, pattern, g % 16, wave, lane));
+    const int flat = g * kWaves + wave;  // load index within this workgroup's walk
+    const int step = flat / 8, i = flat % 8;
+    const int blk = static_cast<int>(blockIdx.x) + (step / 16) * static_cast<int>(gridDim.x);
+    return reinterpret_cast<const u32x4*>(at(w + static_cast<int64_t>(blk) * 128 * 1024, pattern, step % 16, i, lane));
   };
   uint32_t acc = 0;
   int g = 0;
@@ -86,6 +91,7 @@ __global__ __launch_bounds__(64 * kWaves) void ldg_read(const uint8_t* w, int pa
   if (acc == 0x9E3779B9u) sink[0] = static_cast<int>(acc);  // keeps the loads
 }
 
+template <int WAVES, int AHEAD>
 float gbps(bool dma, int pattern, const uint8_t* w, int* sink) {
   hipEvent_t ev[27];
   for (auto& e : ev)
@@ -96,7 +102,7 @@ float gbps(bool dma, int pattern, const uint8_t* w, int* sink) {
     if (dma)
       hipLaunchKernelGGL(dma_read, dim3(256), dim3(64), kDepth * 8192, 0, src, pattern, sink);
     else
-      hipLaunchKernelGGL(ldg_read, dim3(256), dim3(64 * kWaves), 0, 0, src, pattern, sink);
+      hipLaunchKernelGGL((ldg_read<WAVES, AHEAD>), dim3(256), dim3(64 * WAVES), 0, 0, src, pattern, sink);
   }
   if (hipEventRecord(ev[24]) != hipSuccess || hipEventSynchronize(ev[24]) != hipSuccess) return -1.0f;
   // per-launch times from consecutive events
@@ -125,11 +131,14 @@ int main() {
     return 1;
   }
   if (hipMemset(w, 1, 8 * kBytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) return 1;
-  const float d0 = gbps(true, 0, w, sink), d1 = gbps(true, 1, w, sink);
-  const float l0 = gbps(false, 0, w, sink), l1 = gbps(false, 1, w, sink);
+  const float d0 = gbps<8, 4>(true, 0, w, sink), d1 = gbps<8, 4>(true, 1, w, sink);
+  const float l0 = gbps<8, 4>(false, 0, w, sink), l1 = gbps<8, 4>(false, 1, w, sink);
   printf("dma (LDS DMA, 1 wave, 6 steps ahead): 16 rows x 64 B %.0f GB/s, 1 KB rows %.0f GB/s\n", d0, d1);
   printf("ldg (registers, 8 waves, 4 ahead):    16 rows x 64 B %.0f GB/s, 1 KB rows %.0f GB/s\n", l0, l1);
+  const float c84 = l1, c88 = gbps<8, 8>(false, 1, w, sink), c164 = gbps<16, 4>(false, 1, w, sink),
+              c168 = gbps<16, 8>(false, 1, w, sink);
+  printf("ldg 1 KB rows: 8 waves x 4 ahead %.0f, 8 x 8 %.0f, 16 x 4 %.0f, 16 x 8 %.0f GB/s\n", c84, c88, c164, c168);
   (void)hipFree(w);
   (void)hipFree(sink);
-  return d0 > 0 && d1 > 0 && l0 > 0 && l1 > 0 ? 0 : 1;
+  return d0 > 0 && d1 > 0 && l0 > 0 && l1 > 0 && c88 > 0 && c164 > 0 && c168 > 0 ? 0 : 1;
 }
