@@ -238,6 +238,28 @@ def test_hot_expert_spans_many_tiles(mfma_on, encoding):
     close(got2, ref2, f"dropped ids {encoding}")
 
 
+def test_48_route_tiles(mfma_on):
+    """Q4, 32 experts x 1024 rows, 300 tokens top-4: 37.5 routes per expert on
+    average, so the routed projections take 48-route tiles (3 x 16 tokens per
+    MFMA item; every expert's rows x 32 experts fill the 256 CUs). One expert
+    takes ~30% of the tokens (three tiles, the last one partial); the others
+    fill 25-46 of one tile. Against the oracle and the GEMV path."""
+    ext = mfma_on
+    shape = syn.MoEShape("tile48", 2048, 32, 4, 1024)
+    note("mfma 48-route tiles")
+    layer = syn.build_experts(shape, seed=11)
+    dl = to_dev(layer)
+    t = 300
+    x = syn.hidden_states(shape, t, seed=11)
+    idx, w = routes(t, 4, shape.num_experts, 13, hot=3, hot_share=0.3)
+    counts = torch.bincount(idx.flatten(), minlength=shape.num_experts)
+    assert 32 < idx.numel() / shape.num_experts <= 48 and counts.max() > 96 and counts.min() > 0
+    got, got_g = both_paths(ext, lambda: ext.moe_forward(dl, x.to(DEV), idx.to(DEV), w.to(DEV)))
+    ref = om.streaming_reference(x, idx, w, 0, syn.DeviceLayerReader({0: layer}), num_experts=shape.num_experts)
+    close(got, ref, "48-route tiles")
+    close(got, got_g, "48-route tiles mfma vs gemv", rel=5e-3, mx=1e-2)
+
+
 @pytest.mark.parametrize("t", [2, 16, 32])
 def test_qwen_block_batched_decode(mfma_on, t):
     """c2 shapes at batch 2, 16 and 32: router, routed Q4 experts and the BF16

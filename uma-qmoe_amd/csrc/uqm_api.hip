@@ -149,7 +149,7 @@ int nb_for(int enc, double mean_routes) {
 MfmaPlan plan_mfma(int enc, int nmat, int64_t rows, int64_t K, int nb, int64_t tiles, int cus, int max_split) {
   MfmaPlan p;
   p.nb = nb;
-  if (nb <= 2 && (nmat == 1 || enc == UQM_Q4) && rows % 128 == 0 && rows / 128 * tiles >= cus) {
+  if (nb <= 3 && (nmat == 1 || enc == UQM_Q4) && rows % 128 == 0 && rows / 128 * tiles >= cus) {
     p.mw = 8;
     return p;
   }
@@ -195,6 +195,14 @@ int routed_tile_tokens(const uqm_expert_weights* w, int64_t T, int64_t k) {
   const int64_t active = R < w->num_experts ? R : w->num_experts;
   const double mean = static_cast<double>(R) / static_cast<double>(active);
   if (routed_uses_stream(w) && R <= g_opt_stream_max_routes.load(std::memory_order_relaxed)) return 0;
+  // 48-route tiles when most experts would otherwise take a second, nearly
+  // empty 32-route tile (every tile costs a full pass over the expert's rows)
+  // and both Q4 projections run 128-row items (the only kernels built for them)
+  const int cus = device_cus();
+  if (mean > 32 && mean <= 48 && w->encoding == UQM_Q4 && w->intermediate_size % 128 == 0 &&
+      w->hidden_size % 128 == 0 && active * (w->intermediate_size / 128) >= cus &&
+      active * (w->hidden_size / 128) >= cus)
+    return 48;
   return 16 * (mean >= 16 ? 2 : nb_for(w->encoding, mean));
 }
 

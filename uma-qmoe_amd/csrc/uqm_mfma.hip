@@ -183,7 +183,9 @@ struct MfmaCfg {
   static constexpr int W_INSTR = MW * AT * L;  // 1 KB loads per step
   static constexpr int X_INSTR = X_BYTES / 1024;
   static constexpr int I_STEP = W_INSTR + X_INSTR;
-  static constexpr int D = BUF <= 12 * 1024 ? 6 : (BUF <= 32 * 1024 ? 4 : 3);
+  // ring depth: 48-route gate/up tiles (28 KB steps) keep 3 buffers so that
+  // the ring, three scale slots and the metadata fit the 160 KB of LDS
+  static constexpr int D = BUF <= 12 * 1024 ? 6 : (BUF <= 24 * 1024 || (BUF <= 32 * 1024 && NB != 3) ? 4 : 3);
   static constexpr int NL = (D - 2) * I_STEP > 63 ? 2 : 1;  // loader waves
   static constexpr int I_WAVE = I_STEP / NL;
   static constexpr int THREADS = 64 * (MW + NL);
@@ -598,7 +600,12 @@ hipError_t launch_nb(const MfmaArgs& a, int nb, int cus, hipStream_t stream) {
   if (nb <= 1) return launch_cfg<ENC, NMAT, MW, 1, KW>(a, cus, stream);
   if constexpr (KW == 1) {
     if (nb <= 2) return launch_cfg<ENC, NMAT, MW, 2, KW>(a, cus, stream);
+    if constexpr (MW == 8) {
+      // 48-route tiles; the kernel's tile size must equal the tile list's
+      if (nb == 3) return launch_cfg<ENC, NMAT, MW, 3, KW>(a, cus, stream);
+    }
     if constexpr (MW == 4) {
+      if (nb == 3) return hipErrorInvalidValue;
       if (nb <= 4 || ENC != kBF16) return launch_cfg<ENC, NMAT, MW, 4, KW>(a, cus, stream);
       if constexpr (ENC == kBF16) return launch_cfg<ENC, NMAT, MW, 8, KW>(a, cus, stream);
     }
@@ -636,7 +643,7 @@ hipError_t launch_expert_mfma(int enc, int nmat, const MfmaArgs& args, int nb, i
   if (kw != 1 && kw != 4) return hipErrorInvalidValue;
   if (mw != 4 && mw != 8) return hipErrorInvalidValue;
   if (kw == 4 && (nb > 1 || mw != 4)) return hipErrorInvalidValue;
-  if (mw == 8 && nb > 2) return hipErrorInvalidValue;
+  if (mw == 8 && nb > 3) return hipErrorInvalidValue;
   const int wgr = 16 * mw / kw;
   if (a.rows % wgr != 0) return hipErrorInvalidValue;
   if ((a.w_tail != nullptr || (a.rows_valid > 0 && a.rows_valid != a.rows)) && wgr != 16) return hipErrorInvalidValue;
