@@ -379,6 +379,11 @@ int run_routed(const uqm_expert_weights* w, const uint16_t* hidden, int64_t T, i
     g.out = at<uint16_t>(ws, L.h_routed);
     g.ldo = I;
     g.ksplit = 1;
+    // gate/up: row blocks fastest when most experts have one tile (c4 gate/up
+    // 194 vs 229 MB fetched per call for 184 MB of weights); hot experts with
+    // many tiles (c5) share their rows with tiles fastest (53 vs 60 MB for 40)
+    g.order = kOrderAuto;
+    g.active_count = at<int32_t>(ws, L.counters);
     const MfmaPlan pg = plan_mfma(w->encoding, 2, I, H, nb, active, cus, 1);
     int rc = hip_check(launch_expert_mfma(w->encoding, 2, g, pg.nb, pg.kw, pg.mw, cus, stream), "gate/up MFMA launch");
     if (rc) return rc;
@@ -395,6 +400,7 @@ int run_routed(const uqm_expert_weights* w, const uint16_t* hidden, int64_t T, i
     d.out = at<float>(ws, L.y_routed);
     d.ldo = H;
     d.part_stride = R * H;
+    d.order = kOrderRowFastest;
     const MfmaPlan pd = plan_mfma(w->encoding, 1, H, I, nb, active, cus, T > 1 ? kMaxSplit : 1);
     d.ksplit = pd.ksplit;
     *parts = pd.ksplit;

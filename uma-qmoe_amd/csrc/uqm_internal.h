@@ -85,7 +85,14 @@ struct MfmaArgs {
   int64_t part_stride;  // elements between K-split partial outputs
   int32_t ksplit;       // workgroups along K (kModeF32 only)
   int32_t row_blocks;   // set by the launcher
+  // Order of the (row block, route tile) work items: kOrderTileFastest shares
+  // an expert's rows between its tiles, kOrderRowFastest shares a tile's
+  // activations between the row blocks, kOrderAuto takes row blocks fastest
+  // when the device tile list has fewer than 1.5 tiles per active expert.
+  int32_t order;
+  const int32_t* active_count;  // device count of active experts (kOrderAuto)
 };
+constexpr int kOrderTileFastest = 0, kOrderRowFastest = 1, kOrderAuto = 2;
 
 bool mfma_supported(int enc, int64_t rows, int64_t K, int64_t group);
 // nmat 2 = gate/up with the SiLU epilogue (bf16 out), 1 = FP32 rows. nb: 16-route

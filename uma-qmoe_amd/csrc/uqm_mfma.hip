@@ -202,12 +202,17 @@ struct MfmaCfg {
 
 // Persistent workgroups: the (row block, route tile) work items are split into
 // 8 contiguous ranges, one per XCD (blockIdx % 8), and each XCD's range is
-// dealt out round robin over its workgroups. Items run tile fastest, so the
-// tiles of one expert (or of the shared expert) that share a row block run at
-// the same time on neighbouring workgroups of one XCD, which read its weight
-// rows once from HBM and share them through that XCD's L2 (c4: 205 vs 217 us
-// per call with contiguous runs per workgroup, whose second pass over a row
-// block found it evicted; c5 76 vs 79 us). A workgroup loads the metadata of
+// dealt out round robin over its workgroups. With tiles fastest, the tiles of
+// one expert (or of the shared expert) that share a row block run at the same
+// time on neighbouring workgroups of one XCD, which read its weight rows once
+// from HBM and share them through that XCD's L2 (c4: 205 vs 217 us per call
+// with contiguous runs per workgroup, whose second pass over a row block found
+// it evicted; c5 76 vs 79 us). With row blocks fastest, the row blocks of one
+// tile run together and share its gathered activations instead, and each
+// XCD reads only its own tiles' activations: the routed down projection's
+// per-route inputs are larger than an XCD's L2 (c4 5.8 MB), which tiles
+// fastest fetched from HBM by every XCD (c4 down 192 vs 99 MB per call for
+// 92 MB of weights, c5 60 vs 28 MB for 20 MB). A workgroup loads the metadata of
 // all its items into LDS once; after that its loader waves stream the items'
 // steps back to back through the LDS ring, and the MMA waves write each
 // item's outputs when its last step is done.
@@ -256,9 +261,12 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
   const int lane = tid & 63;
 
   // ---- metadata of the run into LDS (every wave takes part in the barriers) ----
+  bool row_fastest = a.order == kOrderRowFastest;
+  if (a.order == kOrderAuto && a.tiles != nullptr && a.active_count != nullptr)
+    row_fastest = 2 * n_tiles < 3 * *a.active_count;
   for (int i = tid; i < nit; i += C::THREADS) {
     const int item = xb + wslot + i * per;
-    const int tile = item % n_tiles;
+    const int tile = row_fastest ? item / a.row_blocks : item % n_tiles;
     int expert = 0, rbeg, nt;
     if (a.tiles != nullptr) {
       expert = a.tiles[2 * tile];
@@ -272,7 +280,7 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
     m[0] = expert;
     m[1] = rbeg;
     m[2] = nt;
-    m[3] = item / n_tiles;
+    m[3] = row_fastest ? item % a.row_blocks : item / n_tiles;
   }
   __syncthreads();
   for (int idx = tid; idx < nit * NTOK; idx += C::THREADS) {
