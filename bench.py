@@ -793,7 +793,9 @@ def main() -> int:
         src = torch.empty(args.copy_probe, dtype=torch.uint8, device="cuda:0").fill_(1)
         dst = torch.empty_like(src)
         for _ in range(8):
-            dst.copy_(src)
+            # an elementwise kernel (x ^ 0): a device-to-device copy_ may go to
+            # a DMA engine, which the counters do not see
+            torch.bitwise_xor(src, 0, out=dst)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": args.copy_probe, "copies": 8}), flush=True)
         return 0
