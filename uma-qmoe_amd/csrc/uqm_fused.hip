@@ -339,31 +339,6 @@ __device__ __forceinline__ void lds_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#define UQM_MAXSTEP(O) v = max(v, static_cast<uint32_t>(__float_as_int(xor_partner<O>(__int_as_float(static_cast<int>(v))))))
-  UQM_MAXSTEP(32);
-  UQM_MAXSTEP(16);
-  UQM_MAXSTEP(8);
-  UQM_MAXSTEP(4);
-  UQM_MAXSTEP(2);
-  UQM_MAXSTEP(1);
-#undef UQM_MAXSTEP
-  return v;
-}
-
-// Order-preserving 16-bit key of a bf16 value: larger value, larger key; -0
-// and +0 share a key; NaN sorts above +inf (as a descending torch.sort puts
-// it first). Keys of non-NaN values are >= 0x007F, so 0 marks "taken".
-__device__ __forceinline__ uint32_t bf16_key(uint16_t u) {
-  if ((u & 0x7FFFu) > 0x7F80u) return 0xFFFFu;
-  if (u == 0x8000u) u = 0;
-  return (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
-}
-__device__ __forceinline__ float bf16_of_key(uint32_t key) {
-  const uint32_t u = (key & 0x8000u) ? (key & 0x7FFFu) : (~key & 0xFFFFu);
-  return bf16_to_f32(static_cast<uint16_t>(u));
-}
-
 // [lo, hi) of n items split evenly over `parts`.
 // (part * n must fit in 32 bits: parts <= 8192 waves, n <= 2^18.)
 __device__ __forceinline__ int split_at(int n, int part, int parts) {

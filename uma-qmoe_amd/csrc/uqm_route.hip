@@ -52,41 +52,34 @@ __device__ __forceinline__ void topk_token(int64_t t, int lane, const uint16_t* 
     if (logits_out != nullptr && e < E) logits_out[t * E + e] = f32_to_bf16(v);
     mx = fmaxf(mx, v);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  mx = wave_max(mx);
   float se = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     if (lane + 64 * i < E) se += __expf(l[i] - mx);
   se = wave_sum(se);
 
-  unsigned used = 0;
-  float my_v = -INFINITY;
+  // Top-k by k rounds of a wave max over (value key, 0xFFFF - id): the
+  // largest logit wins, equal logits go to the lower expert id, NaN sorts
+  // first (as in a descending torch.sort); the exchanges run on DPP and the
+  // permlane swaps, not through LDS.
+  uint32_t key[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    key[i] = e < E ? (bf16_key(f32_to_bf16(l[i])) << 16) | static_cast<uint32_t>(0xFFFF - e) : 0u;
+  }
+  float my_v = 0.f;
   int my_e = -1;
   for (int s = 0; s < k; ++s) {
-    float bv = -INFINITY;
-    int be = 0x7FFFFFFF;
+    uint32_t m = max(max(key[0], key[1]), max(key[2], key[3]));
+    m = wave_max_u32(m);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && !(used & (1u << i)) && (l[i] > bv || (l[i] == bv && e < be))) {
-        bv = l[i];
-        be = e;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, kWave);
-      const int oe = __shfl_xor(be, o, kWave);
-      if (ov > bv || (ov == bv && oe < be)) {
-        bv = ov;
-        be = oe;
-      }
-    }
-    if ((be & 63) == lane) used |= 1u << (be >> 6);
+    for (int i = 0; i < 4; ++i)
+      if (key[i] == m) key[i] = 0u;
     if (lane == s) {
-      my_v = bv;
-      my_e = be;
+      my_e = 0xFFFF - static_cast<int>(m & 0xFFFFu);
+      my_v = bf16_of_key(m >> 16);
     }
   }
   float p = lane < k ? __expf(my_v - mx) / se : 0.f;
