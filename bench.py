@@ -60,6 +60,17 @@ def parse_args():
     return ap.parse_args()
 
 
+def counter_collection_active(environ=None) -> bool:
+    """Whether this process runs under rocprofv3 hardware-counter collection
+    (--pmc or a counter input file), which sets ROCPROF_COUNTER_COLLECTION and
+    ROCPROF_COUNTERS / ROCPROF_COUNTER_GROUPS in the profiled program's
+    environment."""
+    env = os.environ if environ is None else environ
+    flag = str(env.get("ROCPROF_COUNTER_COLLECTION", "")).strip().lower()
+    return flag not in ("", "0", "false", "no", "off") or bool(env.get("ROCPROF_COUNTERS")) or bool(
+        env.get("ROCPROF_COUNTER_GROUPS"))
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -205,7 +216,7 @@ def layer_flops(shape, tokens: int, routes: int) -> float:
 def zipf_routes(torch, syn, shape, x, dense):
     """Top-k routes of a Zipf-biased router (c5): logits = bf16(x W_r^T + b).
     Only the workload's routing pattern matters here, not tie order."""
-    bias = syn.zipf_router_bias(shape, 2.0, device=x.device)
+    bias = syn.zipf_router_bias(shape, device=x.device)
     vals = (torch.nn.functional.linear(x, dense.router).float() + bias).to(torch.bfloat16).float()
     idx = torch.topk(vals, shape.top_k, dim=-1).indices
     w = torch.softmax(vals, -1).gather(-1, idx).to(torch.bfloat16)
@@ -787,6 +798,12 @@ def main() -> int:
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         return 2
+    if counter_collection_active() and not args.copy_probe:
+        print("bench.py refuses to run under rocprofv3 counter collection (--pmc): a FETCH_SIZE run of it once "
+              "stopped for 180 s while building its layer instances and the cause is not known. Take counters "
+              "with the standalone programs (uma-qmoe_amd/lib/fused_timeline, uma-qmoe_amd/lib/grouped_counters) "
+              "or calibrate with --copy-probe.", file=sys.stderr)
+        return 3
     import torch
 
     if args.copy_probe:

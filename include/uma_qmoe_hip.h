@@ -26,8 +26,13 @@
  *     single-token fused kernel's error word and one launch epoch per
  *     workgroup, advanced by every launch, and a completion counter that
  *     multi-token calls leave at zero). Calls in order on one stream may
- *     reuse a workspace, also with different token counts; calls that
- *     overlap in time must not share one.
+ *     reuse a workspace, also with different token counts and shapes (a
+ *     fused launch whose shape differs from the last call's on the same
+ *     workspace first zeroes its hand-off words with a small kernel); calls
+ *     that overlap in time must not share one. The library tracks that last
+ *     shape on the host: a captured graph replays its launches as captured,
+ *     so calls of another shape on the same workspace between replays of a
+ *     graph that holds fused launches need a workspace of their own.
  *   - Return 0 on success, nonzero UQM_ERR_* otherwise; the message is in
  *     uqm_last_error() (thread-local). Invalid arguments are rejected before
  *     any launch.
@@ -65,9 +70,14 @@ enum {
                                       library-owned side stream (one per device, default priority),
                                       forked from and joined back into the caller's stream with
                                       events; 0: everything in order on the caller's stream */
-  UQM_OPT_STREAM_MAX_ROUTES = 5    /* multi-token calls with at most this many routes (tokens x top_k;
+  UQM_OPT_STREAM_MAX_ROUTES = 5,   /* multi-token calls with at most this many routes (tokens x top_k;
                                       default 32, 0 = never) run the routed projections as
                                       expert-grouped streaming GEMVs instead of MFMA grouped GEMMs */
+  UQM_OPT_FUSED_WAIT_US = 6        /* wall-clock budget of the fused kernel's inter-workgroup waits in
+                                      microseconds (default 2000). 0 makes every wait give up at its
+                                      first check, ready or not: each fused launch then takes its
+                                      expired path (poisoned outputs, error word raised) and ends
+                                      normally; for tests of that path */
 };
 
 /* Routed-expert weights of one MoE layer (device pointers). */
@@ -197,12 +207,14 @@ int uqm_set_option(int option, int64_t value);
 
 /* Synchronously reads (and clears) the sticky error word that the fused
  * single-token kernel raises when one of its inter-workgroup waits runs past
- * its wall-clock budget (2 ms from the start of each wave; a launch takes
- * ~20 us). That can only happen when its grid is not fully resident, e.g.
- * while another kernel holds CUs. Such a launch still ends within the budget,
- * and its output is poisoned rather than silently wrong: NaN output rows, and
- * routes -1 / weights NaN when the routing itself expired. Returns UQM_OK when
- * clean. No counterpart in the reference. */
+ * its wall-clock budget (UQM_OPT_FUSED_WAIT_US, 2 ms from the start of each
+ * wave by default; a launch takes ~20 us), together with the word that marks
+ * the launch in which that happened. That can only happen when its grid is
+ * not fully resident, e.g. while another kernel holds CUs. Such a launch
+ * still ends within the budget, and its output is poisoned rather than
+ * silently wrong: NaN output rows, and routes -1 / weights NaN when the
+ * routing itself expired. Returns UQM_OK when clean. No counterpart in the
+ * reference. */
 int uqm_workspace_status(void* workspace, size_t workspace_bytes, void* stream);
 
 /* Scratch bytes uqm_moe_layer_noalloc holds per device (16 MiB: c2 shapes up
@@ -223,6 +235,14 @@ int uqm_workspace_status(void* workspace, size_t workspace_bytes, void* stream);
  * uqm_moe_layer, with the same kernels and results. */
 int uqm_moe_layer_noalloc(const uqm_layer_weights* layer, const void* hidden, int64_t tokens, void* output,
                           void* logits, void* routing_weights, int64_t* expert_indices, void* stream);
+
+/* uqm_workspace_status for the scratch array of uqm_moe_layer_noalloc on the
+ * current device: reads and clears its error word (and expired-launch word)
+ * on `stream`, synchronously. UQM_OK when clean or when no no-allocation
+ * call has run on this device yet. No counterpart in the reference; it lets
+ * callers of uqm_moe_layer_noalloc, who have no workspace pointer, learn that
+ * a fused launch's output was poisoned. */
+int uqm_noalloc_status(void* stream);
 
 /* RMSNorm (Transformers Qwen2MoeRMSNorm, modeling_qwen2_moe.py:65-70): bf16 in/out,
  * FP32 variance; weight bf16 [H] or NULL for ones. Used by the 24-layer stack driver. */

@@ -77,7 +77,7 @@ def case_inputs(name: str):
     x = syn.hidden_states(shape, tokens, seed=SEED, tag=f"golden_{name}")
     if norm:
         x = om.rmsnorm(x, 1e-6)
-    bias = syn.zipf_router_bias(shape, 2.0, seed=SEED) if shape.zipf_s else None
+    bias = syn.zipf_router_bias(shape, seed=SEED) if shape.zipf_s else None
     return shape, layer, dense, x, layer_index, bias
 
 
@@ -103,7 +103,7 @@ def main(names=None) -> None:
         shape, layer, dense, x, layer_index, bias = case_inputs(name)
         out, logits, weights, indices = oracle_case(shape, layer, dense, x, layer_index, bias)
         meta = {"case": name, "shape": asdict(shape), "tokens": int(x.shape[0]), "layer_index": layer_index,
-                "seed": SEED, "zipf_bias_scale": 2.0 if bias is not None else None,
+                "seed": SEED, "zipf_bias_scale": 1.0 if bias is not None else None,
                 "weights_sha256": weights_digest(layer, dense),
                 "generator": "uma_qmoe_amd.synthetic (torch CPU generators), oracle.moe.qwen_block"}
         np.savez_compressed(HERE / f"{name}.npz", meta=np.array(json.dumps(meta, sort_keys=True)), x=_bits(x),

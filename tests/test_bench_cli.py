@@ -88,3 +88,21 @@ def test_cpu_baseline_rows_on_a_tiny_layer():
     assert agreement is None
     assert row["kind"] == "port" and row["cores"] >= 1 and row["value"] > 0
     assert row["predequantized"]["value"] > 0 and row["cpu_model"]
+
+
+def test_counter_collection_is_refused():
+    """Under rocprofv3 counter collection bench.py exits before touching a
+    device (counters are taken with the standalone programs), except for the
+    copy probe that calibrates them."""
+    import os
+
+    bench = _bench_module()
+    assert bench.counter_collection_active({"ROCPROF_COUNTER_COLLECTION": "1"})
+    assert bench.counter_collection_active({"ROCPROF_COUNTER_COLLECTION": "True"})
+    assert bench.counter_collection_active({"ROCPROF_COUNTERS": "pmc: FETCH_SIZE"})
+    assert not bench.counter_collection_active({"ROCPROF_COUNTER_COLLECTION": "0"})
+    assert not bench.counter_collection_active({"ROCPROF_KERNEL_TRACE": "1"})
+    env = dict(os.environ, ROCPROF_COUNTER_COLLECTION="True", ROCPROF_COUNTERS="pmc: FETCH_SIZE")
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--steps", "5"], cwd=ROOT, capture_output=True,
+                       text=True, timeout=120, env=env)
+    assert r.returncode == 3 and "counter collection" in r.stderr and r.stdout == ""

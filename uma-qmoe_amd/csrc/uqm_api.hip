@@ -8,6 +8,7 @@
 #include <atomic>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 
 #include "../../include/uma_qmoe_hip.h"
 #include "uqm_internal.h"
@@ -87,6 +88,7 @@ P* at(void* ws, size_t off) {
 
 // Process-wide options (uqm_set_option).
 std::atomic<int64_t> g_opt_fused{1};
+std::atomic<int64_t> g_opt_fused_wait_us{uqm::kFusedWaitBudgetUs};
 std::atomic<int64_t> g_opt_mfma_min_tokens{2};
 std::atomic<int64_t> g_opt_overlap_shared{1};
 std::atomic<int64_t> g_opt_stream_max_routes{32};
@@ -111,22 +113,63 @@ int device_cus() {
 }
 
 // The fused kernel's wait budget in s_memrealtime ticks of the current device
-// (cached per device id; the clock runs at hipDeviceAttributeWallClockRate kHz).
-std::atomic<int64_t> g_wait_ticks[64];
+// (UQM_OPT_FUSED_WAIT_US; the clock runs at hipDeviceAttributeWallClockRate
+// kHz, cached per device id). A zero budget stays zero: every wait of the
+// launch then gives up at its first check.
+std::atomic<int> g_clock_khz[64];
 
 uint64_t fused_wait_ticks() {
+  const int64_t us = g_opt_fused_wait_us.load(std::memory_order_relaxed);
+  if (us <= 0) return 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = -1;
-  if (dev >= 0 && dev < 64) {
-    const int64_t v = g_wait_ticks[dev].load(std::memory_order_relaxed);
-    if (v > 0) return static_cast<uint64_t>(v);
+  int khz = dev >= 0 && dev < 64 ? g_clock_khz[dev].load(std::memory_order_relaxed) : 0;
+  if (khz <= 0) {
+    if (dev < 0 || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0)
+      khz = 100000;  // the 100 MHz reference clock of CDNA parts
+    if (dev >= 0 && dev < 64) g_clock_khz[dev].store(khz, std::memory_order_relaxed);
   }
-  int khz = 0;
-  if (dev < 0 || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0)
-    khz = 100000;  // the 100 MHz reference clock of CDNA parts
-  const int64_t ticks = static_cast<int64_t>(khz) * uqm::kFusedWaitBudgetUs / 1000;
-  if (dev >= 0 && dev < 64) g_wait_ticks[dev].store(ticks, std::memory_order_relaxed);
-  return static_cast<uint64_t>(ticks);
+  return static_cast<uint64_t>(khz) * static_cast<uint64_t>(us) / 1000u;
+}
+
+// Layout of the fused kernel's hand-off words (shared SiLU products, routed
+// SiLU products, router logits) in a workspace: their offsets and extent
+// depend on these four sizes only. Every entry point that writes into a
+// workspace records the layout it used; a fused launch whose layout differs
+// from the last one recorded for its workspace (or on a workspace not seen
+// before) first zeroes its hand-off region. Words another layout left there
+// (tagged words at other offsets, route tables, partial sums) could otherwise
+// carry the new launch's epoch in both halves of a pair by chance and be
+// taken as this launch's products. Within one layout every fused launch
+// rewrites every hand-off word it reads, so its words always carry the
+// previous launch's epoch and the 16-bit epoch can wrap safely.
+struct HandoffLayout {
+  int64_t E, k, I, Is;
+  bool operator==(const HandoffLayout& o) const { return E == o.E && k == o.k && I == o.I && Is == o.Is; }
+};
+std::mutex g_layout_mu;
+std::unordered_map<uintptr_t, HandoffLayout> g_layouts;  // workspace address -> last layout
+constexpr size_t kMaxTrackedWorkspaces = 4096;           // beyond: forget all (each is cleared once more)
+
+// Records `lay` for `workspace`; for a fused launch, zeroes the hand-off
+// region on `s` first when the layout changed.
+int note_layout(void* workspace, const Layout& L, HandoffLayout lay, bool fused, hipStream_t s) {
+  bool clear = false;
+  {
+    std::lock_guard<std::mutex> lock(g_layout_mu);
+    const uintptr_t key = reinterpret_cast<uintptr_t>(workspace);
+    auto it = g_layouts.find(key);
+    clear = fused && (it == g_layouts.end() || !(it->second == lay));
+    if (it != g_layouts.end()) {
+      it->second = lay;
+    } else {
+      if (g_layouts.size() >= kMaxTrackedWorkspaces) g_layouts.clear();
+      g_layouts.emplace(key, lay);
+    }
+  }
+  if (!clear) return UQM_OK;
+  return hip_check(uqm::launch_zero_fill(at<unsigned char>(workspace, L.fused_hs), L.normed - L.fused_hs, s),
+                   "hand-off region clear");
 }
 
 // Launch shape of one MFMA grouped GEMM (see launch_expert_mfma).
@@ -608,6 +651,7 @@ int uqm_route_permute(const int64_t* expert_indices, int64_t tokens, int64_t top
   const Layout L = layout(tokens, 8, 8, 0, num_experts, top_k);
   if (workspace == nullptr || workspace_bytes < L.total)
     return fail(UQM_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
+  if ((rc = note_layout(workspace, L, {num_experts, top_k, 8, 0}, false, static_cast<hipStream_t>(stream)))) return rc;
   RouteTables rt{at<int32_t>(workspace, L.route_expert), at<int32_t>(workspace, L.route_order),
                  at<int32_t>(workspace, L.expert_offsets), at<int32_t>(workspace, L.active_experts),
                  at<int32_t>(workspace, L.counters), at<int32_t>(workspace, L.tiles),
@@ -634,6 +678,7 @@ int uqm_router_topk(const void* hidden, int64_t tokens, int64_t hidden_size, con
   if (workspace == nullptr || workspace_bytes < L.total)
     return fail(UQM_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, L.total);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((rc = note_layout(workspace, L, {num_experts, top_k, 8, 0}, false, s))) return rc;
   if (router_uses_mfma(hidden_size, tokens))
     return run_router_mfma(router, nullptr, num_experts, static_cast<const uint16_t*>(hidden), tokens, hidden_size,
                            top_k, norm_topk_prob, L, workspace, static_cast<uint16_t*>(routing_weights),
@@ -680,9 +725,11 @@ int uqm_moe_forward(const uqm_expert_weights* weights, const void* hidden, int64
   const int64_t H = weights->hidden_size, I = weights->intermediate_size, E = weights->num_experts;
   // One or two tokens: the fused single-token kernel with the caller's routes
   // (no router), one launch per token.
-  if (tokens <= kFusedMaxTokens && g_opt_fused.load(std::memory_order_relaxed) != 0 &&
-      fused_config_id(weights->encoding, H, I, 0, top_k, E) >= 0 &&
-      (weights->encoding == UQM_BF16 || (H % weights->group_size == 0 && I % weights->group_size == 0))) {
+  const bool fused = tokens <= kFusedMaxTokens && g_opt_fused.load(std::memory_order_relaxed) != 0 &&
+                     fused_config_id(weights->encoding, H, I, 0, top_k, E) >= 0 &&
+                     (weights->encoding == UQM_BF16 || (H % weights->group_size == 0 && I % weights->group_size == 0));
+  if ((rc = note_layout(workspace, L, {E, top_k, I, 0}, fused, s))) return rc;
+  if (fused) {
     FusedArgs fa{};
     fa.eg = static_cast<const uint8_t*>(weights->gate);
     fa.eu = static_cast<const uint8_t*>(weights->up);
@@ -781,9 +828,11 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
   // One or two tokens: one persistent launch per token for the whole block
   // (two tokens: 2 x 20.7 us against 57.9 us on the multi-launch path for c2
   // shapes; three: 62.1 against 63.1).
-  if (tokens <= kFusedMaxTokens && g_opt_fused.load(std::memory_order_relaxed) != 0 &&
-      fused_config_id(w->encoding, H, w->intermediate_size, Is, k, E) >= 0 &&
-      (w->encoding == UQM_BF16 || (H % w->group_size == 0 && w->intermediate_size % w->group_size == 0))) {
+  const bool fused = tokens <= kFusedMaxTokens && g_opt_fused.load(std::memory_order_relaxed) != 0 &&
+                     fused_config_id(w->encoding, H, w->intermediate_size, Is, k, E) >= 0 &&
+                     (w->encoding == UQM_BF16 || (H % w->group_size == 0 && w->intermediate_size % w->group_size == 0));
+  if ((rc = note_layout(workspace, L, {E, k, w->intermediate_size, Is}, fused, s))) return rc;
+  if (fused) {
     FusedArgs fa{};
     fa.x = x;
     fa.rms = norm.rms ? 1 : 0;
@@ -993,6 +1042,10 @@ int uqm_set_option(int option, int64_t value) {
       if (value < 0) return fail(UQM_ERR_ARGUMENT, "routes threshold must be >= 0");
       g_opt_stream_max_routes.store(value);
       return UQM_OK;
+    case UQM_OPT_FUSED_WAIT_US:
+      if (value < 0 || value > 10000000) return fail(UQM_ERR_ARGUMENT, "wait budget must be in [0, 10^7] us");
+      g_opt_fused_wait_us.store(value);
+      return UQM_OK;
     default:
       return fail(UQM_ERR_ARGUMENT, "unknown option %d", option);
   }
@@ -1001,18 +1054,22 @@ int uqm_set_option(int option, int64_t value) {
 int uqm_workspace_status(void* workspace, size_t workspace_bytes, void* stream) {
   if (workspace == nullptr || workspace_bytes < 4 * uqm::kSyncWords)
     return fail(UQM_ERR_WORKSPACE, "workspace is NULL or too small");
-  uint32_t word = 0;
+  static_assert(uqm::kSyncExpired == uqm::kSyncError + 1, "error and expired words are adjacent");
+  uint32_t words[2] = {0, 0};  // error word, expired-launch word
   uint32_t* dev = static_cast<uint32_t*>(workspace) + uqm::kSyncError;
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc;
-  if ((rc = hip_check(hipMemcpyAsync(&word, dev, 4, hipMemcpyDeviceToHost, s), "status read"))) return rc;
+  if ((rc = hip_check(hipMemcpyAsync(words, dev, 8, hipMemcpyDeviceToHost, s), "status read"))) return rc;
   if ((rc = hip_check(hipStreamSynchronize(s), "status sync"))) return rc;
-  if (word == 0) return UQM_OK;
-  const uint32_t zero = 0;
-  if ((rc = hip_check(hipMemcpyAsync(dev, &zero, 4, hipMemcpyHostToDevice, s), "status clear"))) return rc;
+  if (words[0] == 0 && words[1] == 0) return UQM_OK;
+  const uint32_t zero[2] = {0, 0};
+  if ((rc = hip_check(hipMemcpyAsync(dev, zero, 8, hipMemcpyHostToDevice, s), "status clear"))) return rc;
   if ((rc = hip_check(hipStreamSynchronize(s), "status sync"))) return rc;
-  return fail(UQM_ERR_HIP, "a fused launch on this workspace hit its wait bound (error word %u): its output is invalid",
-              word);
+  if (words[0] == 0) return UQM_OK;  // only a stale expired marker: cleared
+  return fail(UQM_ERR_HIP,
+              "a fused launch on this workspace hit its wait bound (error word %u, launch tag %u): its output is "
+              "invalid",
+              words[0], words[1]);
 }
 
 int uqm_rmsnorm(const void* input, int64_t rows, int64_t hidden_size, const void* weight, float eps, void* output,

@@ -45,7 +45,9 @@
 // Its result is poisoned, never silently wrong: routes taken from an
 // incomplete logit poll make the workgroup publish NaN products, and a wave
 // whose product staging expired writes NaN output rows (with routes -1 and
-// weights NaN from workgroup 0 when its own poll expired).
+// weights NaN from workgroup 0 when its own poll expired). Every wave that
+// gives up raises the error word; workgroup 0 removes expired markers of
+// earlier launches at the end of each launch.
 //
 // Each lane streams fixed 16-byte column chunks of every row (non-temporal
 // loads: each weight byte is read once) against activation fragments held in
@@ -403,6 +405,10 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   UQM_FUSED_TRACE_INIT
   UQM_FUSED_TRACE(0);
   const uint64_t deadline = wall_clock() + a.wait_ticks;
+  // A zero budget (a host option for tests of the poisoning path) makes every
+  // wait give up at its first check, ready or not, so that each launch takes
+  // the expired path on every workgroup and still ends normally.
+  const bool force_expiry = a.wait_ticks == 0;
   uint32_t* const my_epoch = a.sync + kSyncEpochBase + b;
   const int group = ER::kScaled ? a.group : 1;
   const int nrow = E + (kShared ? 1 : 0);  // router rows + the shared-expert gate row
@@ -466,6 +472,14 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
       build_fragments();
       lds_barrier();  // routed fragments built
       if (lane == 0) co_store<uint32_t>(my_epoch, epoch);
+      // An expired marker left by an earlier launch is taken out (it would
+      // otherwise make the waits of the launch that reaches the same 16-bit
+      // epoch again give up at once). The marker of this launch stays: the
+      // compare-and-swap cannot remove a value stored after the load.
+      if (b == 0 && lane == 0) {
+        const uint32_t old = co_load(a.sync + kSyncExpired);
+        if (old != 0u && old != epoch) atomicCAS(a.sync + kSyncExpired, old, 0u);
+      }
     };
     if (a.routes_in != nullptr) {
       // Routes given by the caller (the routed-only ops, no shared expert):
@@ -542,7 +556,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
       __builtin_amdgcn_s_sleep(kPollSleep);
       poll(pc);
       for (;;) {
-        if (ready(pa)) {
+        if (!force_expiry && ready(pa)) {
           take(pa);
           break;
         }
@@ -597,7 +611,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
         __builtin_amdgcn_s_sleep(kPollSleepRoutedOnly);
         poll(pc);
         for (;;) {
-          if (ready(pa)) {
+          if (!force_expiry && ready(pa)) {
             take(pa);
             break;
           }
@@ -940,7 +954,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   auto finish_round = [&](const uint64_t* src, int n2, int base, uint32_t* dst, uint64_t (&v)[SL]) {
     // The first check is outside the retry loop, so the compiler waits for
     // exactly these loads (not for the rows issued after them).
-    if (!round_ok(n2, base, v)) {
+    if (force_expiry || !round_ok(n2, base, v)) {
       for (;;) {
         if (wall_clock() > deadline) {
           raise_expired(a.sync, epoch);
@@ -948,6 +962,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
           break;
         }
         if (co_load(a.sync + kSyncExpired) == epoch) {
+          raise_expired(a.sync, epoch);  // the error word is raised by every wave that gives up
           if (lane == 0) *l_stale = 1;
           break;
         }

@@ -192,6 +192,9 @@ hipError_t launch_moe_decode_fused(int enc, const FusedArgs& a, hipStream_t stre
 
 hipError_t launch_rmsnorm(const uint16_t* x, int64_t rows, int64_t H, const uint16_t* weight, float eps,
                           uint16_t* out, hipStream_t stream);
+// Zeroes `bytes` (a multiple of 16) at the 16-byte aligned device address p,
+// with a kernel (no hipMemsetAsync, so that it can be captured into a graph).
+hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t stream);
 
 // Entry-point plumbing shared by the translation units that export C-ABI
 // functions (uqm_api.hip): sets the thread's uqm_last_error message and

@@ -103,3 +103,22 @@ hipError_t launch_rmsnorm(const uint16_t* x, int64_t rows, int64_t H, const uint
 }
 
 }  // namespace uqm
+
+namespace uqm {
+
+__global__ __launch_bounds__(256) void zero_fill_kernel(uint4* __restrict__ p, size_t n16) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n16;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t stream) {
+  if (bytes == 0) return hipSuccess;
+  if ((reinterpret_cast<uintptr_t>(p) & 15u) != 0 || bytes % 16 != 0) return hipErrorInvalidValue;
+  const size_t n16 = bytes / 16;
+  const unsigned blocks = static_cast<unsigned>(n16 / 256 + 1 < 1024 ? n16 / 256 + 1 : 1024);
+  hipLaunchKernelGGL(zero_fill_kernel, dim3(blocks), dim3(256), 0, stream, static_cast<uint4*>(p), n16);
+  return hipGetLastError();
+}
+
+}  // namespace uqm

@@ -27,12 +27,6 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
 
-__global__ void zero_fill_kernel(uint4* p, size_t n16) {
-  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n16;
-       i += static_cast<size_t>(gridDim.x) * blockDim.x)
-    p[i] = make_uint4(0u, 0u, 0u, 0u);
-}
-
 constexpr int kMaxDevices = 64;
 void* g_scratch[kMaxDevices];  // device address of `scratch` per device, set once
 std::mutex g_scratch_mu;
@@ -56,8 +50,7 @@ int device_scratch(hipStream_t s, void** out) {
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr)
       return uqm::api_fail(UQM_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-    hipLaunchKernelGGL(zero_fill_kernel, dim3(1024), dim3(256), 0, s, static_cast<uint4*>(p), kScratchBytes / 16);
-    e = hipGetLastError();
+    e = uqm::launch_zero_fill(p, kScratchBytes, s);
     if (e != hipSuccess) return uqm::api_fail(UQM_ERR_HIP, "scratch fill launch: %s", hipGetErrorString(e));
     g_scratch[dev] = p;
   }
@@ -88,4 +81,17 @@ extern "C" int uqm_moe_layer_noalloc(const uqm_layer_weights* layer, const void*
   }
   return uqm::moe_layer_on_workspace(layer, hidden, tokens, output, logits, routing_weights, expert_indices, ws,
                                      kScratchBytes, /*side_stream=*/false, stream);
+}
+
+extern "C" int uqm_noalloc_status(void* stream) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return uqm::api_fail(UQM_ERR_HIP, "no current device (or device id >= %d)", kMaxDevices);
+  void* ws = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ws = g_scratch[dev];
+  }
+  if (ws == nullptr) return UQM_OK;  // nothing has run on this device's scratch
+  return uqm_workspace_status(ws, kScratchBytes, stream);
 }

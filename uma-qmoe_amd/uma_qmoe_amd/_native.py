@@ -25,6 +25,8 @@ UQM_OPT_MFMA_MIN_TOKENS = 3
 NOALLOC_SCRATCH_BYTES = 16 << 20  # UQM_NOALLOC_SCRATCH_BYTES
 UQM_OPT_OVERLAP_SHARED = 4
 UQM_OPT_STREAM_MAX_ROUTES = 5
+UQM_OPT_FUSED_WAIT_US = 6  # fused kernel's wait budget in microseconds (0: every wait gives up at once)
+FUSED_WAIT_US_DEFAULT = 2000
 
 ENCODING_IDS = {"q4_group128": UQM_Q4, "q8_group128": UQM_Q8, "bf16_le": UQM_BF16}
 
@@ -128,6 +130,7 @@ SIGNATURES = {
     "uqm_rmsnorm": (ctypes.c_int, (_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _vp)),
     "uqm_set_option": (ctypes.c_int, (ctypes.c_int, _i64)),
     "uqm_workspace_status": (ctypes.c_int, (_vp, ctypes.c_size_t, _vp)),
+    "uqm_noalloc_status": (ctypes.c_int, (_vp,)),
     "uqm_pack_open": (ctypes.c_int, (_cp, _i32, _cp, _cp, _cp, _cp, ctypes.POINTER(_vp))),
     "uqm_pack_close": (ctypes.c_int, (_vp,)),
     "uqm_pack_info": (ctypes.c_int, (_vp, _i32p, _u64p, _u64p, _i32p)),

@@ -3,9 +3,9 @@
 Each ``csrc/*.hip`` translation unit (hipcc) and each host-only
 ``csrc/*.cpp`` one (g++) is compiled in parallel to an object under
 ``_build/`` and linked into ``uma-qmoe_amd/lib/libuma_qmoe_hip.so``;
-``csrc/timeline/fused_timeline.hip`` becomes the program
-``uma-qmoe_amd/lib/fused_timeline`` and each ``csrc/probes/NAME.hip`` the
-measurement program ``uma-qmoe_amd/lib/NAME``.
+each ``csrc/timeline/NAME.hip`` (the per-phase timeline of the fused kernel
+and the grouped-GEMM counter program, both used to take rocprofv3 counters
+on a few hundred dispatches) becomes the program ``uma-qmoe_amd/lib/NAME``.
 Run as ``python -m uma_qmoe_amd.build`` with ``uma-qmoe_amd`` on sys.path.
 """
 
@@ -63,30 +63,19 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-TIMELINE_SRC = CSRC / "timeline" / "fused_timeline.hip"
-TIMELINE_PATH = LIB_DIR / "fused_timeline"
+PROGRAMS = CSRC / "timeline"
+# Programs that call the library through its C ABI (linked against it, so
+# built after it); the others include the kernel sources they measure.
+LINKED_PROGRAMS = {"grouped_counters"}
 
 
-def _compile_timeline() -> Path:
-    """The per-phase timeline program of the single-token fused kernel
-    (csrc/timeline/fused_timeline.hip includes csrc/uqm_fused.hip)."""
-    tmp = TIMELINE_PATH.with_suffix(".tmp")
-    cmd = [HIPCC, *[f for f in COMMON_FLAGS if f != "-fPIC"], str(TIMELINE_SRC), "-o", str(tmp)]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {TIMELINE_SRC.name}:\n{proc.stderr}")
-    os.replace(tmp, TIMELINE_PATH)
-    return TIMELINE_PATH
-
-
-PROBES = CSRC / "probes"
-
-
-def _compile_probe(src: Path) -> Path:
-    """A stand-alone measurement program (csrc/probes/NAME.hip -> lib/NAME)."""
+def _compile_program(src: Path) -> Path:
+    """A stand-alone counter program (csrc/timeline/NAME.hip) -> lib/NAME."""
     out = LIB_DIR / src.stem
     tmp = out.with_suffix(".tmp")
     cmd = [HIPCC, *[f for f in COMMON_FLAGS if f != "-fPIC"], str(src), "-o", str(tmp)]
+    if src.stem in LINKED_PROGRAMS:
+        cmd += [f"-L{LIB_DIR}", "-luma_qmoe_hip", "-Wl,-rpath,$ORIGIN"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
@@ -96,7 +85,7 @@ def _compile_probe(src: Path) -> Path:
 
 def build(verbose: bool = False) -> Path:
     """Compile every HIP source, link the shared library and build the
-    timeline program. Always rebuilds."""
+    counter programs. Always rebuilds."""
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     srcs = sources()
@@ -104,7 +93,8 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     jobs = min(len(srcs) + 1, max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        extras = [pool.submit(_compile_timeline)] + [pool.submit(_compile_probe, p) for p in sorted(PROBES.glob("*.hip"))]
+        programs = sorted(PROGRAMS.glob("*.hip"))
+        extras = [pool.submit(_compile_program, p) for p in programs if p.stem not in LINKED_PROGRAMS]
         objs = list(pool.map(_compile, srcs))
         for e in extras:
             e.result()
@@ -114,6 +104,9 @@ def build(verbose: bool = False) -> Path:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, LIB_PATH)
+    for p in programs:
+        if p.stem in LINKED_PROGRAMS:
+            _compile_program(p)
     if verbose:
         print(f"built {LIB_PATH}")
     return LIB_PATH

@@ -360,6 +360,14 @@ class HipExtension:
         rc = self.lib.uqm_workspace_status(_ptr(workspace), workspace.numel(), _stream_handle(torch, workspace.device))
         _native.check(rc, "uqm_workspace_status")
 
+    def noalloc_status(self, device=None) -> None:
+        """Raises if a fused launch through ``moe_layer_noalloc`` on ``device``
+        (default: the current one) hit its wait bound; clears the report."""
+        torch = self.torch
+        dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        with torch.cuda.device(dev):
+            _native.check(self.lib.uqm_noalloc_status(_stream_handle(torch, dev)), "uqm_noalloc_status")
+
     def rmsnorm(self, hidden, eps=1e-6, weight=None):
         torch = self.torch
         self._check_hidden(hidden)
