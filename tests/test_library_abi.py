@@ -59,7 +59,8 @@ def header_enum_values(header: Path = HEADER) -> dict[str, int]:
 def test_python_constants_match_header_enums():
     values = header_enum_values()
     for name in ("UQM_Q4", "UQM_Q8", "UQM_BF16", "UQM_OPT_FUSED_DECODE",
-                 "UQM_OPT_MFMA_MIN_TOKENS", "UQM_OPT_OVERLAP_SHARED", "UQM_OPT_STREAM_MAX_ROUTES", "UQM_ERR_PACK"):
+                 "UQM_OPT_MFMA_MIN_TOKENS", "UQM_OPT_OVERLAP_SHARED", "UQM_OPT_STREAM_MAX_ROUTES",
+                 "UQM_OPT_FUSED_WAIT_US", "UQM_ERR_PACK"):
         assert values[name] == getattr(_native, name), name
     pack_enums = header_enum_values(INCLUDE / "uma_qmoe_pack.h")
     assert (pack_enums["UQM_PACK_EXPERT"], pack_enums["UQM_PACK_TARGET"]) == (0, 1)

@@ -102,3 +102,76 @@ def test_loader_refusals(checkpoint, tmp_path):
         (e / "model.safetensors.index.json").write_text(json.dumps(index))
         with pytest.raises(ContractError, match=message):
             load_fixed_qwen(e, e / "experts.uqep", model_manifest_sha256=MANIFEST, device="cpu", architecture=ARCH)
+
+
+def _target_pack(path, q4, keep=lambda name: True):
+    """The tiny model's routed experts as a Q4 TargetPack (policy
+    "qwen-tiny-q4", every layer Q4), holding the tensors ``keep`` accepts."""
+    from uma_qmoe_amd.formats import TargetTensor
+    from uma_qmoe_amd.packfile import write_target_pack
+    from uma_qmoe_amd.qwen_host import QWEN_MODEL_ID, QWEN_MODEL_REVISION
+
+    tensors = [(n, TargetTensor(tuple(t.shape), "q4_group128", t.packed, t.scales, t.group_size))
+               for n, t in sorted(q4.items()) if keep(n)]
+    write_target_pack(path, tensors, model_id=QWEN_MODEL_ID, model_revision=QWEN_MODEL_REVISION,
+                      model_manifest_sha256=MANIFEST, policy_id="qwen-tiny-q4",
+                      layer_encodings={i: "q4_group128" for i in range(24)}, policy_evidence_sha256="4" * 64)
+    return path
+
+
+def test_target_pack_loads_and_incomplete_one_is_refused(checkpoint, tmp_path):
+    """A complete TargetPack loads (one mapping, one VMA); one missing a
+    layer, or holding a tensor at the wrong shape, is refused before the model
+    is built (target_pack.py:738-775 via qwen_compressed_loader.py:187)."""
+    d, _pack, _model, q4 = checkpoint
+    full = _target_pack(tmp_path / "full.uqtp", q4)
+    with load_fixed_qwen(d, full, model_manifest_sha256=MANIFEST, device="cpu", architecture=ARCH,
+                         target_policy_id="qwen-tiny-q4") as host:
+        assert host.evidence["expert_pack_mapping_count"] == 1
+        assert host.evidence["expert_pack_vma_count"] == 1
+        assert host.evidence["quantized_moe_block_count"] == 2
+    host.close()  # a second close does nothing
+    partial = _target_pack(tmp_path / "partial.uqtp", q4, keep=lambda n: not n.startswith("model.layers.1."))
+    with pytest.raises(ContractError, match=r"tensor set mismatch: missing=\['model\.layers\.1\.mlp\.experts\.0\."):
+        load_fixed_qwen(d, partial, model_manifest_sha256=MANIFEST, device="cpu", architecture=ARCH,
+                        target_policy_id="qwen-tiny-q4")
+    with pytest.raises(ContractError, match="Qwen TargetPack loading requires a policy id"):
+        load_fixed_qwen(d, full, model_manifest_sha256=MANIFEST, device="cpu", architecture=ARCH)
+
+
+def test_reader_with_more_than_one_mapping_is_refused(checkpoint):
+    from uma_qmoe_amd.packfile import ExpertPackReader
+
+    d, pack, _model, _q4 = checkpoint
+    reader = ExpertPackReader(pack, expected_model_manifest_sha256=MANIFEST)
+    try:
+        reader.mapping_count = 2
+        with pytest.raises(ContractError, match="mapped ExpertPack more than once"):
+            load_fixed_qwen(d, reader, model_manifest_sha256=MANIFEST, device="cpu", architecture=ARCH)
+    finally:
+        reader.close()
+
+
+def test_incomplete_target_pack_counts_are_checked():
+    """The completeness check on an in-memory pack: the exact tensor set at
+    the model's shapes passes; a policy that disagrees with the stored
+    encodings is refused."""
+    from uma_qmoe_amd.formats import encode
+    from uma_qmoe_amd.packfile import memory_pack
+    from uma_qmoe_amd.qwen_host import expected_expert_tensors, require_complete_target_pack
+
+    import numpy as np
+
+    shapes = expected_expert_tensors(2, 3, 256, 128)
+    assert len(shapes) == 2 * 3 * 3 and shapes["model.layers.1.mlp.experts.2.down_proj.weight"] == (256, 128)
+    tensors = {n: encode(np.zeros(s, np.float32), "q4_group128") for n, s in shapes.items()}
+    require_complete_target_pack(memory_pack(tensors, {0: "q4_group128", 1: "q4_group128"}),
+                                 layers=2, experts=3, hidden=256, intermediate=128)
+    with pytest.raises(ContractError, match="policy counts are inconsistent"):
+        require_complete_target_pack(memory_pack(tensors, {0: "q4_group128", 1: "q8_group128"}),
+                                     layers=2, experts=3, hidden=256, intermediate=128)
+    bad = dict(tensors)
+    bad["model.layers.0.mlp.experts.0.up_proj.weight"] = encode(np.zeros((128, 128), np.float32), "q4_group128")
+    with pytest.raises(ContractError, match=r"wrong_shape=\['model\.layers\.0\.mlp\.experts\.0\.up_proj"):
+        require_complete_target_pack(memory_pack(bad, {0: "q4_group128", 1: "q4_group128"}),
+                                     layers=2, experts=3, hidden=256, intermediate=128)

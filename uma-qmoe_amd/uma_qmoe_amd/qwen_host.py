@@ -15,13 +15,14 @@ benchmarks/runners/run_compressed_qwen_baseline.py, decodes eagerly).
 
 from __future__ import annotations
 
+import itertools
 import json
 import re
 from dataclasses import dataclass
 from pathlib import Path
-from typing import Any
+from typing import Any, Iterator, Mapping
 
-from .formats import ContractError
+from .formats import ENCODINGS, ContractError
 
 QWEN_MODEL_ID = "Qwen/Qwen1.5-MoE-A2.7B"
 QWEN_MODEL_REVISION = "1a758c50ecb6350748b9ce0a99d2352fd9fc11c9"  # fixed_models.py:44-55
@@ -126,42 +127,126 @@ def restore_nonpersistent_buffers(model: Any, config: Any, device: Any) -> None:
         raise ContractError("fixed Qwen non-persistent buffers are not initialized")
 
 
-def _partition(weight_map: Any, required: set[str]) -> tuple[dict[str, list[str]], list[str]]:
-    """Dense checkpoint tensors by shard, and the skipped expert tensors
-    (qwen_compressed_loader.py:100-125)."""
-    if not isinstance(weight_map, dict):
-        raise ContractError("fixed Qwen weight_map must be an object")
-    by_shard: dict[str, list[str]] = {}
-    skipped: list[str] = []
-    dense: set[str] = set()
-    for name, shard in weight_map.items():
-        if not isinstance(name, str) or not isinstance(shard, str) or not shard:
+@dataclass(frozen=True)
+class QwenCheckpointIndex:
+    """What a Qwen checkpoint directory's safetensors index says about the
+    tensors a compressed host needs.
+
+    ``dense`` maps every tensor the host model materialises (its state dict)
+    to the shard that holds it; ``experts`` are the per-expert tensors the
+    index lists and the pack replaces. ``read`` refuses an index whose dense
+    set is not exactly the model's (qwen_compressed_loader.py:99-122 keeps
+    the same refusal and message)."""
+
+    root: Path
+    dense: Mapping[str, str]
+    experts: frozenset
+
+    @classmethod
+    def read(cls, root: Path, wanted: set[str]) -> "QwenCheckpointIndex":
+        try:
+            entries = json.loads((root / "model.safetensors.index.json").read_text(encoding="utf-8"))["weight_map"]
+        except (OSError, json.JSONDecodeError, KeyError, TypeError) as exc:
+            raise ContractError("cannot load fixed Qwen Safetensors index") from exc
+        if not isinstance(entries, dict):
+            raise ContractError("fixed Qwen weight_map must be an object")
+        if not all(isinstance(k, str) and isinstance(v, str) and v for k, v in entries.items()):
             raise ContractError("fixed Qwen weight_map entries must be strings")
-        if is_qwen_expert_tensor_name(name):
-            skipped.append(name)
-            continue
-        dense.add(name)
-        by_shard.setdefault(shard, []).append(name)
-    if dense != required:
-        missing = sorted(required - dense)
-        unexpected = sorted(dense - required)
-        raise ContractError(f"fixed Qwen dense checkpoint set mismatch: missing={missing[:8]!r}, "
-                            f"unexpected={unexpected[:8]!r}")
-    return by_shard, skipped
+        experts = frozenset(filter(is_qwen_expert_tensor_name, entries))
+        dense = {name: shard for name, shard in entries.items() if name not in experts}
+        if dense.keys() != wanted:
+            missing, unexpected = sorted(wanted - dense.keys()), sorted(dense.keys() - wanted)
+            raise ContractError(f"fixed Qwen dense checkpoint set mismatch: missing={missing[:8]!r}, "
+                                f"unexpected={unexpected[:8]!r}")
+        return cls(root, dense, experts)
+
+    def tensors(self) -> Iterator[tuple[str, Any]]:
+        """(name, CPU tensor) of every dense tensor, one shard open at a time,
+        shards and names in sorted order."""
+        from safetensors import safe_open
+
+        by_shard: dict[str, list[str]] = {}
+        for name in sorted(self.dense):
+            by_shard.setdefault(self.dense[name], []).append(name)
+        for shard in sorted(by_shard):
+            with safe_open(self.root / shard, framework="pt", device="cpu") as source:
+                for name in by_shard[shard]:
+                    yield name, source.get_tensor(name)
 
 
-@dataclass
+def expected_expert_tensors(layers: int, experts: int, hidden: int, intermediate: int) -> dict[str, tuple[int, int]]:
+    """{name: shape} of the routed-expert tensors of a Qwen MoE model: gate and
+    up [intermediate, hidden], down [hidden, intermediate] per layer and expert
+    (the set target_pack.py:738-775 requires of the fixed model, 24 x 60 x 3)."""
+    shapes = {"gate_proj": (intermediate, hidden), "up_proj": (intermediate, hidden), "down_proj": (hidden, intermediate)}
+    return {f"model.layers.{l}.mlp.experts.{e}.{p}.weight": s
+            for l in range(layers) for e in range(experts) for p, s in shapes.items()}
+
+
+def _tensor_table(reader: Any) -> dict[str, tuple[tuple[int, ...], str]]:
+    """{name: (shape, encoding)} of every tensor of a TargetPack reader (its
+    header's table; an in-memory pack has none and is asked per tensor)."""
+    entries = reader.header.get("tensors")
+    if entries is None:
+        return {n: (tuple(t.shape), t.encoding) for n in reader.names() for t in (reader.tensor(n),)}
+    return {t["name"]: (tuple(t["shape"]), t["encoding"]) for t in entries}
+
+
+def require_complete_target_pack(reader: Any, *, layers: int, experts: int, hidden: int, intermediate: int) -> None:
+    """Refuses a TargetPack that does not hold exactly the model's routed
+    experts at their shapes, or whose per-encoding tensor counts disagree
+    with its layer policy (TargetPackReader.validate_fixed_qwen_complete,
+    target_pack.py:738-775, with the fixed model's sizes as arguments and
+    the same messages)."""
+    want = expected_expert_tensors(layers, experts, hidden, intermediate)
+    table = _tensor_table(reader)
+    have = {name: shape for name, (shape, _enc) in table.items()}
+    if have != want:
+        missing, unexpected = sorted(want.keys() - have.keys()), sorted(have.keys() - want.keys())
+        wrong = sorted(n for n in want.keys() & have.keys() if want[n] != have[n])
+        raise ContractError(f"TargetPack fixed Qwen tensor set mismatch: missing={missing[:8]!r}, "
+                            f"unexpected={unexpected[:8]!r}, wrong_shape={wrong[:8]!r}")
+    per_layer = [reader.layer_encoding(l) for l in range(layers)]
+    policy = {enc: 3 * experts * per_layer.count(enc) for enc in sorted(ENCODINGS)}
+    stored = {enc: sum(e == enc for _shape, e in table.values()) for enc in sorted(ENCODINGS)}
+    declared = reader.header.get("encoding_tensor_counts", stored)
+    if not policy == stored == declared:
+        raise ContractError("TargetPack fixed Qwen policy counts are inconsistent")
+
+
+def pack_vma_count(path: Path | None) -> int:
+    """Memory mappings of ``path`` in this process (/proc/self/maps); -1 when
+    that cannot be read or the pack has no file (compressed_loader.py:125-133)."""
+    if path is None:
+        return -1
+    target = str(Path(path).resolve())
+    try:
+        maps = Path("/proc/self/maps").read_text(encoding="utf-8")
+    except OSError:
+        return -1
+    return sum(line.endswith(target) or f"{target} " in line for line in maps.splitlines())
+
+
 class FixedQwenHost:
-    model: Any
-    expert_pack: Any
-    pack_handle: int
-    evidence: dict[str, Any]
+    """A loaded host model, the pack its MoE blocks read and the pack's
+    operator handle. ``close`` (or leaving the ``with`` block) unregisters
+    the handle — waiting for calls in flight — and closes the pack; a second
+    close does nothing."""
+
+    def __init__(self, model: Any, expert_pack: Any, pack_handle: int, evidence: dict[str, Any]) -> None:
+        self.model = model
+        self.expert_pack = expert_pack
+        self.pack_handle = pack_handle
+        self.evidence = evidence
+        self._open = True
 
     def close(self) -> None:
         from .custom_op import unregister_expert_pack
 
-        unregister_expert_pack(self.pack_handle)
-        self.expert_pack.close()
+        if self._open:
+            self._open = False
+            unregister_expert_pack(self.pack_handle)
+            self.expert_pack.close()
 
     def __enter__(self) -> "FixedQwenHost":
         return self
@@ -170,90 +255,133 @@ class FixedQwenHost:
         self.close()
 
 
-def _open_pack(expert_pack: Any, model_id: str, model_revision: str, manifest: str, policy: str | None) -> Any:
+def _open_pack(expert_pack: Any, model_id: str, model_revision: str, manifest: str,
+               policy: str | None) -> tuple[Any, Path | None]:
+    """The pack reader (opened here from a path, else the reader given) and
+    the file it maps, if known. A TargetPack needs the policy id, an
+    ExpertPack refuses one (qwen_compressed_loader.py:170-195 messages)."""
     from .packfile import ExpertPackReader, TargetPackReader
 
     if not isinstance(expert_pack, (str, Path)):
-        return expert_pack  # an open reader
+        return expert_pack, getattr(expert_pack, "path", None)
     path = Path(expert_pack)
     try:
         with path.open("rb") as f:
-            magic = f.read(8)
+            is_target = f.read(8) == _TARGET_MAGIC
     except OSError as exc:
         raise ContractError(f"cannot read compressed Qwen pack {path}: {exc}") from exc
     expected = dict(expected_model_id=model_id, expected_model_revision=model_revision,
                     expected_model_manifest_sha256=manifest)
-    if magic == _TARGET_MAGIC:
-        if not policy:
-            raise ContractError("Qwen TargetPack loading requires a policy id")
-        return TargetPackReader(path, expected_policy_id=policy, **expected)
-    if policy is not None:
+    if is_target and not policy:
+        raise ContractError("Qwen TargetPack loading requires a policy id")
+    if not is_target and policy is not None:
         raise ContractError("Qwen ExpertPack cannot satisfy a TargetPack policy id")
-    return ExpertPackReader(path, **expected)
+    reader = TargetPackReader(path, expected_policy_id=policy, **expected) if is_target else ExpertPackReader(
+        path, **expected)
+    return reader, path
+
+
+def _host_model(config: Any, pack_handle: int, device: Any, *, performance_mode: bool, fused_block: bool) -> Any:
+    """The Transformers model built on the meta device with every MoE block
+    swapped for the quantized block, then materialised (uninitialised) on
+    ``device`` with its non-persistent buffers rebuilt. No expert parameter
+    is ever allocated."""
+    torch = _torch()
+    from transformers import AutoModelForCausalLM
+
+    with torch.device("meta"):
+        model = AutoModelForCausalLM.from_config(config, dtype=torch.bfloat16, trust_remote_code=False)
+    replace_moe_blocks(model, pack_handle, performance_mode=performance_mode, fused_block=fused_block)
+    model.to_empty(device=device)
+    restore_nonpersistent_buffers(model, config, device)
+    return model
+
+
+def _fill_dense(model: Any, index: QwenCheckpointIndex, device: Any) -> tuple[int, int]:
+    """Copies every dense checkpoint tensor into the model (BF16, the
+    destination's shape); returns (tensor count, bytes)."""
+    torch = _torch()
+    slots = model.state_dict(keep_vars=True)
+    count = nbytes = 0
+    with torch.no_grad():
+        for name, value in index.tensors():
+            if value.dtype != torch.bfloat16:
+                raise ContractError(f"dense tensor {name!r} is not BF16")
+            slot = slots[name]
+            if slot.shape != value.shape:
+                raise ContractError(f"dense tensor {name!r} shape mismatch")
+            slot.copy_(value.to(device=device))
+            count += 1
+            nbytes += value.numel() * value.element_size()
+    if count != len(slots):
+        raise ContractError("not every Qwen dense checkpoint tensor was loaded")
+    return count, nbytes
 
 
 def load_fixed_qwen(model_directory: str | Path, expert_pack: Any, *, model_manifest_sha256: str,
                     device: str = "cuda:0", performance_mode: bool = False, target_policy_id: str | None = None,
                     fused_block: bool = True, architecture: tuple = QWEN_ARCHITECTURE,
                     model_id: str = QWEN_MODEL_ID, model_revision: str = QWEN_MODEL_REVISION) -> FixedQwenHost:
-    """Dense Qwen BF16 tensors from a local checkpoint directory plus one
-    expert pack (qwen_compressed_loader.py:143-299). ``expert_pack`` is a pack
-    file path or an open reader; ``architecture`` is the (model_type,
-    layers, experts, top-k) the checkpoint must have (the fixed model's by
-    default)."""
+    """A Qwen MoE host: the dense BF16 tensors of a local checkpoint directory
+    in a Transformers model whose MoE blocks run the HIP operator over one
+    expert pack (the fixed-model loader of qwen_compressed_loader.py:143-299,
+    with the same refusals and evidence keys). ``expert_pack`` is a pack file
+    or an open reader; ``architecture`` is the (model_type, layers, experts,
+    top-k) the checkpoint must have, the fixed model's by default.
+
+    The pack is checked before anything is built: one mapping (one VMA when
+    its file is known) and, for a TargetPack, exactly the model's routed
+    experts. The model's layout is then fixed by the config, the dense
+    tensors are streamed shard by shard, and the result is checked: every
+    block replaced, every dense tensor loaded, the index's expert tensors
+    all skipped, no expert or meta tensor left."""
     torch = _torch()
-    from safetensors import safe_open
-    from transformers import AutoConfig, AutoModelForCausalLM
+    from transformers import AutoConfig
 
     from .custom_op import register_expert_pack, register_moe_forward, unregister_expert_pack
+    from .packfile import MemoryTargetPack, TargetPackReader
 
     root = Path(model_directory)
     config = AutoConfig.from_pretrained(root, local_files_only=True, trust_remote_code=False)
-    observed = (getattr(config, "model_type", None), getattr(config, "num_hidden_layers", None),
-                getattr(config, "num_experts", None), getattr(config, "num_experts_per_tok", None))
-    if observed != tuple(architecture):
-        raise ContractError(f"unexpected fixed Qwen architecture {observed!r}")
-    reader = _open_pack(expert_pack, model_id, model_revision, model_manifest_sha256, target_policy_id)
+    arch = tuple(getattr(config, f, None) for f in ("model_type", "num_hidden_layers", "num_experts",
+                                                     "num_experts_per_tok"))
+    if arch != tuple(architecture):
+        raise ContractError(f"unexpected fixed Qwen architecture {arch!r}")
+    _model_type, layers, experts, _top_k = arch
+    reader, pack_path = _open_pack(expert_pack, model_id, model_revision, model_manifest_sha256, target_policy_id)
+    opened_here = isinstance(expert_pack, (str, Path))
+    try:
+        if getattr(reader, "mapping_count", None) != 1:
+            raise ContractError("compressed Qwen host mapped ExpertPack more than once")
+        vmas = pack_vma_count(pack_path)
+        if vmas not in (1, -1):
+            raise ContractError("compressed Qwen host observed multiple ExpertPack VMAs")
+        if isinstance(reader, (TargetPackReader, MemoryTargetPack)):
+            require_complete_target_pack(reader, layers=layers, experts=experts, hidden=config.hidden_size,
+                                         intermediate=config.moe_intermediate_size)
+    except BaseException:
+        if opened_here:
+            reader.close()
+        raise
     register_moe_forward()
     handle = register_expert_pack(reader)
     try:
-        with torch.device("meta"):
-            model = AutoModelForCausalLM.from_config(config, dtype=torch.bfloat16, trust_remote_code=False)
-        replaced = replace_moe_blocks(model, handle, performance_mode=performance_mode, fused_block=fused_block)
-        model.to_empty(device=device)
-        restore_nonpersistent_buffers(model, config, device)
-        try:
-            weight_map = json.loads((root / "model.safetensors.index.json").read_text(encoding="utf-8"))["weight_map"]
-        except (OSError, json.JSONDecodeError, KeyError) as exc:
-            raise ContractError("cannot load fixed Qwen Safetensors index") from exc
-        required = set(model.state_dict())
-        by_shard, skipped = _partition(weight_map, required)
-        loaded: set[str] = set()
-        dense_bytes = 0
-        params, buffers = dict(model.named_parameters()), dict(model.named_buffers())
-        with torch.no_grad():
-            for shard in sorted(by_shard):
-                with safe_open(root / shard, framework="pt", device="cpu") as source:
-                    for name in sorted(by_shard[shard]):
-                        value = source.get_tensor(name)
-                        if value.dtype != torch.bfloat16:
-                            raise ContractError(f"dense tensor {name!r} is not BF16")
-                        destination = params[name] if name in params else buffers[name]
-                        if tuple(destination.shape) != tuple(value.shape):
-                            raise ContractError(f"dense tensor {name!r} shape mismatch")
-                        destination.copy_(value.to(device=device))
-                        dense_bytes += value.numel() * value.element_size()
-                        loaded.add(name)
-        if loaded != required:
-            raise ContractError("not every Qwen dense checkpoint tensor was loaded")
-        layers, experts = architecture[1], architecture[2]
-        if len(skipped) != layers * experts * 3:
-            raise ContractError(f"expected to skip {layers * experts * 3} Qwen expert tensors, "
-                                f"skipped {len(skipped)}")
-        if any(".mlp.experts." in name for name, _ in model.named_parameters()):
-            raise ContractError("compressed Qwen host still contains expert Parameters")
-        if any(p.is_meta for p in model.parameters()) or any(b.is_meta for b in model.buffers()):
-            raise ContractError("compressed Qwen host contains meta tensors")
+        model = _host_model(config, handle, device, performance_mode=performance_mode, fused_block=fused_block)
+        index = QwenCheckpointIndex.read(root, set(model.state_dict()))
+        dense_count, dense_bytes = _fill_dense(model, index, device)
+        blocks = sum(isinstance(layer.mlp, _BLOCK) for layer in model.model.layers)
+        expert_params = [n for n, _ in model.named_parameters() if ".mlp.experts." in n]
+        failures = [
+            (blocks != layers, "compressed Qwen host did not replace every MoE block"),
+            (len(index.experts) != layers * experts * 3,
+             f"expected to skip {layers * experts * 3} Qwen expert tensors, skipped {len(index.experts)}"),
+            (bool(expert_params), "compressed Qwen host still contains expert Parameters"),
+            (any(t.is_meta for t in itertools.chain(model.parameters(), model.buffers())),
+             "compressed Qwen host contains meta tensors"),
+        ]
+        for failed, message in failures:
+            if failed:
+                raise ContractError(message)
         model.eval()
         evidence = {
             "model_id": model_id,
@@ -261,21 +389,25 @@ def load_fixed_qwen(model_directory: str | Path, expert_pack: Any, *, model_mani
             "device": str(device),
             "performance_mode": performance_mode,
             "fused_block": fused_block,
-            "dense_tensor_count": len(loaded),
+            "dense_tensor_count": dense_count,
             "dense_tensor_bytes": dense_bytes,
-            "skipped_expert_tensor_count": len(skipped),
+            "skipped_expert_tensor_count": len(index.experts),
             "loaded_expert_tensor_count": 0,
-            "expert_parameter_count": 0,
-            "quantized_moe_block_count": replaced,
-            "expert_pack_mapping_count": getattr(reader, "mapping_count", 1),
+            "expert_parameter_count": len(expert_params),
+            "quantized_moe_block_count": blocks,
             "model_parameter_bytes": sum(p.numel() * p.element_size() for p in model.parameters()),
+            "expert_pack_mapping_count": reader.mapping_count,
+            "expert_pack_vma_count": vmas,
         }
-        if replaced != layers:
-            raise ContractError("compressed Qwen host did not replace every MoE block")
+        if pack_path is not None:
+            evidence["expert_pack_size_bytes"] = Path(pack_path).stat().st_size
+        if str(device).startswith("cuda"):
+            evidence["torch_allocated_bytes"] = int(torch.cuda.memory_allocated(device))
+            evidence["torch_reserved_bytes"] = int(torch.cuda.memory_reserved(device))
         return FixedQwenHost(model, reader, handle, evidence)
     except BaseException:
         unregister_expert_pack(handle)
-        if isinstance(expert_pack, (str, Path)):
+        if opened_here:
             reader.close()
         raise
 
