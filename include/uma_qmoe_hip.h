@@ -249,6 +249,17 @@ int uqm_noalloc_status(void* stream);
 int uqm_rmsnorm(const void* input, int64_t rows, int64_t hidden_size, const void* weight, float eps,
                 void* output, void* stream);
 
+/* output[i] = bf16(q_i * scales[i / group_size]) (FP32 product, rounded to
+ * nearest even) for the `elements` values of an encoded Q4 or Q8 tensor
+ * (flattened; a multiple of 8; group_size a multiple of 8): the transient
+ * dequantisation of the reference's correctness path, dequantize_q4 /
+ * decode_target_tensor then .to(bfloat16) (src/uma_qmoe/q4.py:168-179,
+ * src/uma_qmoe/target_pack.py:144-176, src/uma_qmoe/custom_op.py:416-431).
+ * The library's performance_mode=False path runs the routed experts on
+ * BF16 copies made with it; nothing keeps them after the call. */
+int uqm_dequantize(int32_t encoding, const void* data, const float* scales, int64_t elements,
+                   int64_t group_size, void* output, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,7 +12,9 @@ cuda tensors, and compare with the oracle reading the same pack:
 
 Also: the backend's cache summary equals the staged compressed bytes with no
 dequantized cache, unregistering empties the caches, ``q4_linear`` through a
-pack handle, correctness mode runs only a registered implementation, and the
+pack handle, correctness mode (the library's transient-dequantisation path, or a
+registered implementation in its place), the HIP dequantisation bit for bit
+against the oracle codec, and the
 multi-token routing weights equal softmax(logits) at the selected experts.
 Tolerance (north star): rel-L2 <= 1e-2, max-abs <= 2e-2; indices bit-exact
 given the logits.
@@ -158,20 +160,42 @@ def test_c2_qwen_ops_from_target_pack_file(tmp_path, norm):
     assert backend.cache_summary()["tensor_count"] == 0
 
 
-def test_correctness_mode_runs_the_registered_implementation(tmp_path):
-    """performance_mode=False runs what register_reference_implementation
-    installed (here the oracle), with the leased reader."""
+def test_correctness_mode_on_the_device(tmp_path):
+    """performance_mode=False on device tensors runs the library's correctness
+    path (experts dequantised transiently to BF16, then the BF16 expert
+    kernels): within the north-star tolerance of the oracle and of performance
+    mode, an invalid expert id refused as the reference refuses it, nothing
+    cached. An implementation installed with register_reference_implementation
+    runs instead (here the oracle), with the leased reader."""
     L = 3
-    shape = syn.MoEShape("ops_small", 2048, 60, 4, 256)
+    shape = syn.MoEShape("ops_small", 2048, 60, 4, 256, 512)
     layer = syn.build_experts(shape, device=DEV, seed=5)
+    dense = syn.build_dense(shape, device=DEV, seed=5)
     reader = _qwen_q4_pack(tmp_path, layer, L)
     handle = register_target_pack(reader)
-    install_packed_q4_backend()
+    backend = install_packed_q4_backend()
     try:
-        x = syn.hidden_states(shape, 3, seed=3)
-        _l, w, idx = om.router(x, syn.build_dense(shape, seed=5).router, 4)
-        with pytest.raises(RuntimeError, match="no registered qwen implementation"):
-            torch.ops.uma_qmoe.qwen_moe_forward(x.to(DEV), idx.to(DEV), w.to(DEV), L, handle, False)
+        for t in (1, 3, 40):
+            note(f"ops correctness mode: qwen_moe_forward and moe_block T={t}")
+            x = syn.hidden_states(shape, t, seed=3 + t)
+            _l, w, idx = om.router(x, dense.router.cpu(), 4)
+            slow = torch.ops.uma_qmoe.qwen_moe_forward(x.to(DEV), idx.to(DEV), w.to(DEV), L, handle, False)
+            fast = torch.ops.uma_qmoe.qwen_moe_forward(x.to(DEV), idx.to(DEV), w.to(DEV), L, handle, True)
+            ref = om.qwen_streaming_reference(x, idx, w, L, reader)
+            assert_close(slow, ref, f"correctness mode vs oracle T={t}")
+            assert_close(fast, slow, f"performance vs correctness mode T={t}")
+            args = (dense.router, dense.shared_gate, dense.shared_up, dense.shared_down, dense.shared_expert_gate, 4,
+                    False, L, handle)
+            out, logits, weights, indices = torch.ops.uma_qmoe.moe_block(x.to(DEV), *args, False)
+            assert_weights_follow_logits(logits, weights, indices, False, f"correctness-mode block T={t}")
+            ref_b, *_ = om.qwen_block(x, {**_dense_cpu(dense), "top_k": 4, "num_experts": 60}, reader, L,
+                                      routes=(weights.cpu(), indices.cpu()))
+            assert_close(out, ref_b, f"correctness-mode moe_block vs oracle T={t}")
+        bad = idx.clone()
+        bad[0, 1] = 60
+        with pytest.raises(RuntimeError, match="invalid expert"):
+            torch.ops.uma_qmoe.qwen_moe_forward(x.to(DEV), bad.to(DEV), w.to(DEV), L, handle, False)
+        assert backend.cache_summary()["dequantized_weight_bytes"] == 0
         seen = []
 
         def oracle_impl(hidden, indices, weights, layer_index, rd):
@@ -180,13 +204,45 @@ def test_correctness_mode_runs_the_registered_implementation(tmp_path):
                 hidden.device)
 
         register_reference_implementation("qwen", oracle_impl)
-        slow = torch.ops.uma_qmoe.qwen_moe_forward(x.to(DEV), idx.to(DEV), w.to(DEV), L, handle, False)
-        fast = torch.ops.uma_qmoe.qwen_moe_forward(x.to(DEV), idx.to(DEV), w.to(DEV), L, handle, True)
+        registered = torch.ops.uma_qmoe.qwen_moe_forward(x.to(DEV), idx.to(DEV), w.to(DEV), L, handle, False)
         assert seen == [reader]
-        assert_close(fast, slow, "performance vs correctness mode")
+        assert torch.equal(registered.cpu(), ref.to(registered.dtype))
     finally:
         unregister_expert_pack(handle)
         reader.close()
+
+
+@pytest.mark.parametrize("encoding", ["q4_group128", "q8_group128"])
+def test_dequantize_bits_match_the_oracle_codec(hip_ext, encoding):
+    """uqm_dequantize against the oracle's C codec then round-to-nearest-even
+    to BF16, bit for bit: random payloads (every code the codec decodes:
+    nibbles -7..7, bytes -128..127), scales of mixed magnitude, and a tensor
+    whose 128-value groups cross its rows (3 x 136). Q4's reserved -8 code,
+    which the codec refuses, decodes to -8 * scale as in every other kernel
+    of the library."""
+    import numpy as np
+
+    from oracle import codec as oc
+
+    rng = np.random.default_rng(11)
+    for shape in ((3, 136), (2, 64, 256)):
+        n = int(np.prod(shape))
+        scales = (rng.uniform(0.5, 2.0, -(-n // 128)) * 10.0 ** rng.integers(-6, 3, -(-n // 128))).astype("<f4")
+        if encoding == "q4_group128":
+            nib = rng.choice(np.array([c for c in range(16) if c != 8], dtype=np.uint8), n)
+            raw = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
+            want = oc.q4_dequantize(raw.tobytes(), scales.tobytes(), shape)
+        else:
+            raw = rng.integers(-128, 128, n, dtype=np.int8)
+            want = oc.q8_dequantize(raw.tobytes(), scales.tobytes(), shape)
+        got = hip_ext.dequantize(torch.from_numpy(raw.copy()).to(DEV), torch.from_numpy(scales).to(DEV), encoding, 128)
+        bits = got.cpu().view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(bits, oc.f32_to_bf16_bits(want)), f"{encoding} {shape}"
+    if encoding == "q4_group128":  # the reserved code: 0x88 is (-8, -8)
+        raw = np.full(64, 0x88, dtype=np.uint8)
+        sc = np.array([0.25], dtype="<f4")
+        got = hip_ext.dequantize(torch.from_numpy(raw).to(DEV), torch.from_numpy(sc).to(DEV), encoding, 128)
+        assert bool((got.cpu().float() == -2.0).all())
 
 
 # ------------------------------------------------------------------ c3 --

@@ -1086,4 +1086,24 @@ int uqm_rmsnorm(const void* input, int64_t rows, int64_t hidden_size, const void
                    "rmsnorm launch");
 }
 
+int uqm_dequantize(int32_t encoding, const void* data, const float* scales, int64_t elements, int64_t group_size,
+                   void* output, void* stream) {
+  using namespace uqm;
+  int rc = check_device();
+  if (rc) return rc;
+  if (encoding != UQM_Q4 && encoding != UQM_Q8)
+    return fail(UQM_ERR_ARGUMENT, "dequantize takes a Q4 or Q8 tensor, not encoding %d", encoding);
+  if (elements < 0 || elements % 8 != 0) return fail(UQM_ERR_ARGUMENT, "element count must be a multiple of 8");
+  if (group_size <= 0 || group_size % 8 != 0)
+    return fail(UQM_ERR_ARGUMENT, "group size %lld must be a positive multiple of 8", (long long)group_size);
+  if (elements == 0) return UQM_OK;
+  if (data == nullptr || scales == nullptr || output == nullptr)
+    return fail(UQM_ERR_ARGUMENT, "data, scales and output are required");
+  if (!aligned16(data) || !aligned16(output) || reinterpret_cast<uintptr_t>(scales) % 4 != 0)
+    return fail(UQM_ERR_ARGUMENT, "data and output must be 16-byte aligned, scales 4-byte aligned");
+  return hip_check(launch_dequantize(encoding == UQM_Q4, data, scales, elements, group_size, output,
+                                     static_cast<hipStream_t>(stream)),
+                   "dequantize launch");
+}
+
 }  // extern "C"

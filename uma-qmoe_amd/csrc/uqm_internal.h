@@ -195,6 +195,10 @@ hipError_t launch_rmsnorm(const uint16_t* x, int64_t rows, int64_t H, const uint
 // Zeroes `bytes` (a multiple of 16) at the 16-byte aligned device address p,
 // with a kernel (no hipMemsetAsync, so that it can be captured into a graph).
 hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t stream);
+// out[i] = bf16(q_i * scales[i / group]) over `elements` (a multiple of 8)
+// values of a Q4 (q4 = true) or Q8 tensor; group a multiple of 8.
+hipError_t launch_dequantize(bool q4, const void* data, const float* scales, int64_t elements, int64_t group,
+                             void* out, hipStream_t stream);
 
 // Entry-point plumbing shared by the translation units that export C-ABI
 // functions (uqm_api.hip): sets the thread's uqm_last_error message and

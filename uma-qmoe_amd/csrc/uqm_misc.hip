@@ -122,3 +122,59 @@ hipError_t launch_zero_fill(void* p, size_t bytes, hipStream_t stream) {
 }
 
 }  // namespace uqm
+
+namespace uqm {
+
+// Dequantisation of an encoded Q4 or Q8 tensor to BF16: out[i] = bf16(q_i *
+// scale[i / group]), the FP32 product rounded to nearest even, as the
+// reference's correctness path builds its transient experts
+// (src/uma_qmoe/q4.py:168-179 dequantize_q4, src/uma_qmoe/target_pack.py:144-176
+// decode_target_tensor, then .to(bfloat16) at src/uma_qmoe/custom_op.py:416-431).
+// Each thread takes 8 consecutive elements: 4 packed bytes (Q4, low nibble
+// first, two's complement) or 8 bytes (Q8), one scale (group % 8 == 0), one
+// 16-byte store.
+template <bool Q4>
+__global__ __launch_bounds__(256) void dequantize_kernel(const uint8_t* __restrict__ data,
+                                                         const float* __restrict__ scales, int64_t n8,
+                                                         int64_t group8, uint4* __restrict__ out) {
+  for (int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; c < n8;
+       c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const float s = scales[c / group8];
+    int q[8];
+    if constexpr (Q4) {
+      const uint32_t w = reinterpret_cast<const uint32_t*>(data)[c];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) q[j] = static_cast<int>((w >> (4 * j)) & 0xFu) - (((w >> (4 * j)) & 0x8u) ? 16 : 0);
+    } else {
+      const uint2 w = reinterpret_cast<const uint2*>(data)[c];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        q[j] = static_cast<int8_t>((w.x >> (8 * j)) & 0xFFu);
+        q[4 + j] = static_cast<int8_t>((w.y >> (8 * j)) & 0xFFu);
+      }
+    }
+    uint32_t h[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      h[j] = static_cast<uint32_t>(f32_to_bf16(static_cast<float>(q[2 * j]) * s)) |
+             (static_cast<uint32_t>(f32_to_bf16(static_cast<float>(q[2 * j + 1]) * s)) << 16);
+    out[c] = make_uint4(h[0], h[1], h[2], h[3]);
+  }
+}
+
+hipError_t launch_dequantize(bool q4, const void* data, const float* scales, int64_t elements, int64_t group,
+                             void* out, hipStream_t stream) {
+  if (elements <= 0) return hipSuccess;
+  const int64_t n8 = elements / 8;
+  const int64_t want = (n8 + 255) / 256;
+  const unsigned blocks = static_cast<unsigned>(want < 8192 ? want : 8192);
+  if (q4)
+    hipLaunchKernelGGL(dequantize_kernel<true>, dim3(blocks), dim3(256), 0, stream, static_cast<const uint8_t*>(data),
+                       scales, n8, group / 8, static_cast<uint4*>(out));
+  else
+    hipLaunchKernelGGL(dequantize_kernel<false>, dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(data), scales, n8, group / 8, static_cast<uint4*>(out));
+  return hipGetLastError();
+}
+
+}  // namespace uqm

@@ -128,6 +128,7 @@ SIGNATURES = {
         (ctypes.POINTER(LayerWeights), _vp, _i64, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp),
     ),
     "uqm_rmsnorm": (ctypes.c_int, (_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _vp)),
+    "uqm_dequantize": (ctypes.c_int, (_i32, _vp, _vp, _i64, _i64, _vp, _vp)),
     "uqm_set_option": (ctypes.c_int, (ctypes.c_int, _i64)),
     "uqm_workspace_status": (ctypes.c_int, (_vp, ctypes.c_size_t, _vp)),
     "uqm_noalloc_status": (ctypes.c_int, (_vp,)),

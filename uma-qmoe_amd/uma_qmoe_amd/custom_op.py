@@ -20,10 +20,14 @@ Different here:
     sigmoid-gated shared expert) as one op, so the router and the shared
     expert run in the same HIP pipeline;
   * the MI355X platform is ``hip_gfx950``;
-  * performance_mode=False runs an explicitly registered correctness
-    implementation (``register_reference_implementation``); none ships with
-    the product, so without one the call raises. The reference instead
-    computes its streaming correctness path there (custom_op.py:509-579).
+  * performance_mode=False on HIP tensors runs the library's correctness
+    path (``native_backend.CorrectnessPath``: the layer's experts dequantised
+    transiently to BF16 by a HIP kernel, then the BF16 expert kernels), as the
+    reference computes its streaming correctness path there
+    (custom_op.py:509-579). An implementation installed with
+    ``register_reference_implementation`` takes its place (tests install the
+    CPU oracle this way); CPU tensors need one, since this build runs no
+    expert arithmetic on the CPU.
 """
 
 from __future__ import annotations
@@ -154,13 +158,9 @@ class PackRegistry:
         with self._cond:
             self.references[kind] = implementation
 
-    def reference(self, kind: str) -> Callable[..., Any]:
+    def reference(self, kind: str) -> Callable[..., Any] | None:
         with self._cond:
-            impl = self.references.get(kind)
-        if impl is None:
-            raise RuntimeError(f"uma_qmoe correctness mode has no registered {kind} implementation; "
-                               "pass performance_mode=True to run the HIP backend")
-        return impl
+            return self.references.get(kind)
 
 
 REGISTRY = PackRegistry()
@@ -204,7 +204,8 @@ def performance_backend(platform: str) -> Any:
 
 
 def register_reference_implementation(kind: str, implementation: Callable[..., Any]) -> None:
-    """Install the correctness implementation of performance_mode=False.
+    """Install the correctness implementation of performance_mode=False, in
+    place of the library's own (which runs on HIP tensors only).
 
     ``kind`` is ``"olmoe"`` (moe_forward), ``"qwen"`` (qwen_moe_forward) or
     ``"block"`` (moe_block). It is called with the op's arguments, the pack
@@ -247,7 +248,15 @@ def _run(kind: str, hidden_states: Any, args: tuple, pack_handle: int, performan
     with REGISTRY.lease(pack_handle) as reader:
         platform = device_platform(torch, hidden_states)
         if not performance_mode:
-            return REGISTRY.reference(kind)(hidden_states, *args, reader)
+            impl = REGISTRY.reference(kind)
+            if impl is not None:
+                return impl(hidden_states, *args, reader)
+            if platform != "hip_gfx950":
+                raise RuntimeError(f"uma_qmoe correctness mode on {platform} tensors has no registered {kind} "
+                                   "implementation; the built-in correctness path runs on hip_gfx950 devices")
+            from .native_backend import correctness_forward
+
+            return correctness_forward(kind, hidden_states, args, reader)
         attr, words = _OPS[kind]
         backend = REGISTRY.backend(platform)
         fn = backend if attr is None else getattr(backend, attr, None)

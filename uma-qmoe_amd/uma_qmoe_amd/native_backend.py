@@ -213,6 +213,36 @@ class HipExtension:
         _native.check(rc, "uqm_bf16_linear")
         return out.reshape(*input_tensor.shape[:-1], out_features)
 
+    # ------------------------------------------------------ dequantisation --
+    def dequantize(self, data, scales, encoding: str, group_size: int):
+        """bf16(q * scale) of every value of an encoded Q4 or Q8 tensor, flat
+        (the library's HIP kernel; the reference's correctness path
+        dequantises the same way, q4.py:168-179 then .to(bfloat16))."""
+        torch = self.torch
+        if encoding not in ("q4_group128", "q8_group128"):
+            raise RuntimeError(f"cannot dequantize a {encoding} tensor")
+        data = data.contiguous()
+        n = data.numel() * (2 if encoding == "q4_group128" else 1)
+        out = torch.empty(n, dtype=torch.bfloat16, device=data.device)
+        rc = self.lib.uqm_dequantize(_native.ENCODING_IDS[encoding], _ptr(data), _ptr(scales.contiguous()), n,
+                                     int(group_size), _ptr(out), _stream_handle(torch, data.device))
+        _native.check(rc, "uqm_dequantize")
+        return out
+
+    def bf16_experts(self, layer: DeviceExperts) -> DeviceExperts:
+        """The layer with every expert dequantised to BF16 (a transient copy:
+        nothing keeps it after the caller drops it); a BF16 layer as is."""
+        if layer.encoding == "bf16_le":
+            return layer
+        E, H, I = layer.num_experts, layer.hidden_size, layer.intermediate_size
+
+        def deq(data, scales, rows, cols):
+            return self.dequantize(data, scales, layer.encoding, layer.group_size).view(E, rows, cols)
+
+        return DeviceExperts("bf16_le", layer.group_size, E, H, I, deq(layer.gate, layer.gate_scales, I, H), None,
+                             deq(layer.up, layer.up_scales, I, H), None, deq(layer.down, layer.down_scales, H, I),
+                             None)
+
     # ------------------------------------------------------------ routing --
     def route_permute(self, expert_indices, num_experts):
         """(route_order int64 [T*k], expert_offsets int64 [E+1]) on the device."""
@@ -594,6 +624,78 @@ def stage_experts(reader: Any, layer_index: int, device: Any, num_experts: int |
         raise RuntimeError(f"layer {layer_index} projection shapes are inconsistent: {shapes}")
     return DeviceExperts(encoding, group, E, hidden, inter, out["gate_proj"][0], out["gate_proj"][1], out["up_proj"][0],
                          out["up_proj"][1], out["down_proj"][0], out["down_proj"][1])
+
+
+class CorrectnessPath:
+    """``performance_mode=False`` on HIP tensors: the reference's correctness
+    path (custom_op.py:172-340 and :343-506: every expert of the layer
+    dequantised transiently to BF16, then BF16 expert GEMMs with FP32
+    accumulation) in this library's kernels. Each call stages the layer's
+    compressed experts from the leased reader, dequantises them with
+    ``uqm_dequantize`` and runs the BF16 expert kernels on them; nothing is
+    cached between calls. The routes are checked on the host first (one
+    synchronisation), as the reference does, so an id outside [0, E) is an
+    error here rather than a route that contributes nothing.
+
+    It shares no state with the performance backends and needs none of them
+    installed; it is not a fallback: a performance-mode call never reaches it.
+    """
+
+    @staticmethod
+    def extension() -> HipExtension:
+        return load_native_extension()[1]
+
+    @classmethod
+    def _experts(cls, reader: Any, layer_index: int, hidden_states: Any) -> DeviceExperts:
+        import torch
+
+        if hidden_states.dtype != torch.bfloat16:
+            raise RuntimeError("uma_qmoe correctness mode requires BF16 hidden states")
+        layer = stage_experts(reader, layer_index, hidden_states.device)
+        if hidden_states.shape[-1] != layer.hidden_size:
+            raise RuntimeError(f"hidden size {hidden_states.shape[-1]} does not match the layer's {layer.hidden_size}")
+        return cls.extension().bf16_experts(layer)
+
+    @classmethod
+    def routed(cls, hidden_states, expert_indices, routing_weights, layer_index, reader):
+        """moe_forward / qwen_moe_forward: out [*, H]."""
+        import torch
+
+        if expert_indices.dtype not in (torch.int32, torch.int64):
+            raise RuntimeError("expert_indices must use int32 or int64")
+        if tuple(expert_indices.shape) != tuple(routing_weights.shape):
+            raise RuntimeError("expert_indices and routing_weights shapes must match")
+        layer = cls._experts(reader, layer_index, hidden_states)
+        flat = hidden_states.reshape(-1, layer.hidden_size)
+        if expert_indices.ndim != 2 or expert_indices.shape[0] != flat.shape[0]:
+            raise RuntimeError("expert_indices must have shape [tokens, top_k]")
+        if expert_indices.numel() and bool(((expert_indices < 0) | (expert_indices >= layer.num_experts)).any()):
+            raise RuntimeError("expert_indices contains an invalid expert")
+        out = cls.extension().moe_forward(layer, flat, expert_indices, routing_weights)
+        return out.reshape(hidden_states.shape)
+
+    @classmethod
+    def block(cls, hidden_states, router_weight, shared_gate_proj, shared_up_proj, shared_down_proj,
+              shared_expert_gate, top_k, norm_topk_prob, layer_index, reader):
+        """moe_block: (out, router logits, routing weights, expert indices)."""
+        import torch
+
+        layer = cls._experts(reader, layer_index, hidden_states)
+        shared = (shared_gate_proj, shared_up_proj, shared_down_proj, shared_expert_gate)
+        if any(t is None for t in shared) and not all(t is None for t in shared):
+            raise RuntimeError("shared expert tensors must be given together")
+        dense = DenseBlock(router_weight.to(torch.bfloat16).contiguous(),
+                           *(None if t is None else t.to(torch.bfloat16).contiguous() for t in shared))
+        if tuple(dense.router.shape) != (layer.num_experts, layer.hidden_size):
+            raise RuntimeError(f"router weight must be [{layer.num_experts}, {layer.hidden_size}]")
+        return cls.extension().moe_layer(layer, dense, hidden_states, int(top_k), bool(norm_topk_prob))
+
+
+def correctness_forward(kind: str, hidden_states: Any, args: tuple, reader: Any) -> Any:
+    """Runs op ``kind`` ("olmoe", "qwen" or "block") in correctness mode on HIP tensors."""
+    if kind == "block":
+        return CorrectnessPath.block(hidden_states, *args, reader)
+    return CorrectnessPath.routed(hidden_states, *args, reader)
 
 
 class _NativeMoEBackend:
