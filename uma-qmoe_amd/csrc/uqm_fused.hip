@@ -932,7 +932,8 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   // launch's epoch, and stores the bf16 pairs. The shared products (published
   // since phase A) are loaded before the phase-C rows, so they are in LDS by
   // the time the shared down row arrives; the routed products are loaded
-  // after them and are the last thing the wave waits for.
+  // after the routed down rows (and, with Q4 rows, after the first part of
+  // the shared down row), so that they are ready when they arrive.
   const uint32_t epoch = next_epoch(last_epoch);
   constexpr int kRound = SL * kWaves * 64;
   auto load_round = [&](const uint64_t* src, int n2, int base, uint64_t (&v)[SL]) {
@@ -991,15 +992,37 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
       finish_round(hs64, n2s, b2, reinterpret_cast<uint32_t*>(lhs), vs);
     }
   };
+  // With Q4 routed rows (job ids in registers) the shared down row goes out
+  // in two parts around the routed-product loads: its first CSA chunks per
+  // lane, the product loads, the rest. The products then arrive while the
+  // rest of the row streams, so their staging and the routed fragments are
+  // built before the row is complete, and only the dot products remain once
+  // it is. A product wait that has to retry re-issues its loads behind the
+  // whole row, which is where the loads sat before (CSA = 3 of 11 chunks:
+  // 22.4-22.8 vs 22.8-23.8 us per launch in the timeline harness; 5: 22.9,
+  // 7: 23.1, 0: 22.9).
+  constexpr bool kSplit = kJobRegs && kShared;
+  constexpr int CSA = kSplit ? 3 : CISX;
+  auto issue_cs_range = [&](int o, auto lo_tag, auto hi_tag) {
+    constexpr int J0 = decltype(lo_tag)::value, J1 = decltype(hi_tag)::value;
+#pragma unroll
+    for (int j = J0; j < J1; ++j)
+      rs.w[j] = ld_stream(a.sd_w + static_cast<int64_t>(o) * rowIS + static_cast<uint32_t>(colIS.c(j) * 16));
+  };
+  uint64_t vr[SL];
   {
     uint64_t vs[SL];
     if constexpr (kShared) load_round(hs64, n2s, base0, vs);
     if constexpr (kJobRegs || !kShared) issue_cr(oa < ob ? oa : H - 1);
-    issue_cs(oa < ob ? oa : H - 1, colIS);
+    if constexpr (kSplit)
+      issue_cs_range(oa < ob ? oa : H - 1, std::integral_constant<int, 0>{}, std::integral_constant<int, CSA>{});
+    else
+      issue_cs(oa < ob ? oa : H - 1, colIS);
     if constexpr (kShared) stage_hs(vs);
   }
-  uint64_t vr[SL];
   load_round(hr64, n2r, base0, vr);
+  if constexpr (kSplit)
+    issue_cs_range(oa < ob ? oa : H - 1, std::integral_constant<int, CSA>{}, std::integral_constant<int, CISX>{});
   UQM_FUSED_TRACE(7);
   lds_barrier();  // shared products staged
 
@@ -1040,7 +1063,8 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     }
     return acc;
   };
-  const float acc_s = shared_part(colIS);
+  float acc_s = 0.f;
+  if constexpr (!kSplit) acc_s = shared_part(colIS);
   if constexpr (!kJobRegs && kShared) issue_cr(oa < ob ? oa : H - 1);
   finish_round(hr64, n2r, base0, reinterpret_cast<uint32_t*>(lhr), vr);
   for (int b2 = base0 + kRound; b2 - lane < n2r; b2 += kRound) {
@@ -1051,6 +1075,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
   build_fragments();
   lds_barrier();  // routed fragments built
   UQM_FUSED_TRACE(8);
+  if constexpr (kSplit) acc_s = shared_part(colIS);  // waits for the rest of the shared down row
   const bool stale = *l_stale != 0;
   // out[o] = bf16(sum over lanes of (shared part + routed part)).
   {
