@@ -9,7 +9,10 @@
 // rotation and prints, per phase boundary, when the waves reached it
 // (microseconds after the first wave of the launch started), averaged over
 // the traced launches. Usage:
-//   fused_timeline [c2|c1] [instances=13] [reps=40]
+//   fused_timeline [c2|c1|c3bf16|c3q8] [instances=13] [reps=40]
+// (c2: Qwen shapes, Q4 routed experts and the BF16 shared expert; c1: OLMoE
+// shapes, Q4, no shared expert; c3bf16 / c3q8: the Qwen stack's BF16 and Q8
+// layers, with the input RMSNorm folded in)
 // Phase boundaries (streaming waves unless noted):
 //   0 entry
 //   1 control wave: router rows published
@@ -89,12 +92,19 @@ int main(int argc, char** argv) {
   const int R = argc > 2 ? atoi(argv[2]) : 13;
   const int reps = argc > 3 ? atoi(argv[3]) : 40;
   const bool c1 = strcmp(config, "c1") == 0;
+  // c3 layer kinds: BF16 routed experts (layers 0-15) or Q8 (16-23), the
+  // input RMSNorm folded in (unit weight), as the 24-layer stack runs them
+  const bool c3b = strcmp(config, "c3bf16") == 0, c3q = strcmp(config, "c3q8") == 0;
+  const int enc = c3b ? uqm::kBF16 : c3q ? uqm::kQ8 : uqm::kQ4;
   const int64_t H = 2048, I = c1 ? 1024 : 1408, Is = c1 ? 0 : 5632;
   const int E = c1 ? 64 : 60, k = c1 ? 8 : 4, G = 128;
-  if (R < 1 || reps < 1) {
-    fprintf(stderr, "usage: fused_timeline [c2|c1] [instances>=1] [reps>=1]\n");
+  if (R < 1 || reps < 1 || !(c1 || c3b || c3q || strcmp(config, "c2") == 0)) {
+    fprintf(stderr, "usage: fused_timeline [c2|c1|c3bf16|c3q8] [instances>=1] [reps>=1]\n");
     return 2;
   }
+  // bytes per routed matrix element and scale words per expert matrix
+  const size_t elem_num = enc == uqm::kQ4 ? 1 : enc == uqm::kQ8 ? 2 : 4, elem_den = 2;
+  const bool scaled = enc != uqm::kBF16;
   const size_t ws_bytes = 1 << 20;
   char* ws = device_alloc<char>(ws_bytes);
   CHECK(hipMemset(ws, 0, ws_bytes));
@@ -106,16 +116,23 @@ int main(int argc, char** argv) {
   for (int r = 0; r < R; ++r) {
     uqm::FusedArgs& a = inst[r];
     memset(&a, 0, sizeof(a));
-    const size_t routed = static_cast<size_t>(E) * I * H / 2, scales = static_cast<size_t>(E) * I * H / G;
+    const size_t routed = static_cast<size_t>(E) * I * H * elem_num / elem_den,
+                 scales = scaled ? static_cast<size_t>(E) * I * H / G : 1;
     uint16_t* router = device_alloc<uint16_t>(E * H);
     fill_bf16(router, E * H, 100 + r);
     uint8_t* eg = device_alloc<uint8_t>(routed);
     uint8_t* eu = device_alloc<uint8_t>(routed);
     uint8_t* ed = device_alloc<uint8_t>(routed);
     float* sc = device_alloc<float>(3 * scales);
-    fill_bytes(eg, routed, 600 + r);
-    fill_bytes(eu, routed, 700 + r);
-    fill_bytes(ed, routed, 800 + r);
+    if (enc == uqm::kBF16) {
+      fill_bf16(eg, routed / 2, 600 + r);
+      fill_bf16(eu, routed / 2, 700 + r);
+      fill_bf16(ed, routed / 2, 800 + r);
+    } else {
+      fill_bytes(eg, routed, 600 + r);
+      fill_bytes(eu, routed, 700 + r);
+      fill_bytes(ed, routed, 800 + r);
+    }
     fill_scales(sc, 3 * scales);
     a.router = reinterpret_cast<const uint8_t*>(router);
     if (Is > 0) {
@@ -135,9 +152,14 @@ int main(int argc, char** argv) {
     a.eg = eg;
     a.eu = eu;
     a.ed = ed;
-    a.egs = sc;
-    a.eus = sc + scales;
-    a.eds = sc + 2 * scales;
+    a.egs = scaled ? sc : nullptr;
+    a.eus = scaled ? sc + scales : nullptr;
+    a.eds = scaled ? sc + 2 * scales : nullptr;
+    if (c3b || c3q) {
+      a.rms = 1;  // RMSNorm(x) with weight ones folded in (uqm_norm_moe_layer)
+      a.rms_w = nullptr;
+      a.rms_eps = 1e-6f;
+    }
     a.x = x;
     a.out = out;
     a.H = H;
@@ -151,8 +173,8 @@ int main(int argc, char** argv) {
     a.hs = reinterpret_cast<uint32_t*>(ws + 8192);
     a.hr = reinterpret_cast<uint32_t*>(ws + 8192 + 4 * 8192);
     a.lgt = reinterpret_cast<uint64_t*>(ws + 8192 + 8 * 8192);
-    bytes_per_call = static_cast<size_t>(k) * (3 * (I * H / 2) + 3 * (I * H / G) * 4) + static_cast<size_t>(E) * H * 2 +
-                     (Is > 0 ? 3 * Is * H * 2 + H * 2 : 0);
+    bytes_per_call = static_cast<size_t>(k) * (3 * (I * H * elem_num / elem_den) + (scaled ? 3 * (I * H / G) * 4 : 0)) +
+                     static_cast<size_t>(E) * H * 2 + (Is > 0 ? 3 * Is * H * 2 + H * 2 : 0);
   }
   CHECK(hipDeviceSynchronize());
   int dev = 0, cus = 0, khz = 0;
@@ -166,10 +188,10 @@ int main(int argc, char** argv) {
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
   for (int w = 0; w < 3; ++w)
-    for (int r = 0; r < R; ++r) CHECK(uqm::launch_moe_decode_fused(uqm::kQ4, inst[r], 0));
+    for (int r = 0; r < R; ++r) CHECK(uqm::launch_moe_decode_fused(enc, inst[r], 0));
   CHECK(hipEventRecord(e0, 0));
   for (int i = 0; i < reps; ++i)
-    for (int r = 0; r < R; ++r) CHECK(uqm::launch_moe_decode_fused(uqm::kQ4, inst[r], 0));
+    for (int r = 0; r < R; ++r) CHECK(uqm::launch_moe_decode_fused(enc, inst[r], 0));
   CHECK(hipEventRecord(e1, 0));
   CHECK(hipEventSynchronize(e1));
   float ms = 0.f;
@@ -183,7 +205,7 @@ int main(int argc, char** argv) {
   for (int r = 0; r < R; ++r) {
     unsigned long long* p = trace + r * per_launch;
     CHECK(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &p, sizeof(p)));
-    CHECK(uqm::launch_moe_decode_fused(uqm::kQ4, inst[r], 0));
+    CHECK(uqm::launch_moe_decode_fused(enc, inst[r], 0));
     CHECK(hipDeviceSynchronize());
   }
   unsigned long long* none = nullptr;
