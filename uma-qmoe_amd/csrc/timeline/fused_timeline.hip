@@ -6,9 +6,12 @@
 // configuration with arbitrary weight bytes (the timing does not depend on
 // the values; every nibble and bf16 pattern decodes to a finite number),
 // times `reps` rotations over them with HIP events, then traces one more
-// rotation and prints, per phase boundary, when the waves reached it
-// (microseconds after the first wave of the launch started), averaged over
-// the traced launches. Usage:
+// rotation launched back to back behind untraced ones (the steady state of
+// the timed loop; each launch gets its own trace region through
+// FusedArgs::trace) and prints the launch-to-launch period, the span of a
+// launch, and per phase boundary when the waves reached it (microseconds
+// after the first wave of the launch started), averaged over the traced
+// launches. Usage:
 //   fused_timeline [c2|c1|c3bf16|c3q8] [instances=13] [reps=40]
 // (c2: Qwen shapes, Q4 routed experts and the BF16 shared expert; c1: OLMoE
 // shapes, Q4, no shared expert; c3bf16 / c3q8: the Qwen stack's BF16 and Q8
@@ -32,9 +35,8 @@
 #include <string.h>
 #include <vector>
 
-__device__ unsigned long long* g_trace;  // [launch wave][16] wall-clock stamps, NULL: off
-
-#define UQM_FUSED_TRACE_INIT unsigned long long* const trace_base_ = g_trace;
+// FusedArgs::trace: [wave][16] wall-clock stamps of one launch, NULL: off
+#define UQM_FUSED_TRACE_INIT unsigned long long* const trace_base_ = a.trace;
 #define UQM_FUSED_TRACE(p)                                                                     \
   do {                                                                                         \
     if ((threadIdx.x & 63) == 0 && trace_base_ != nullptr)                                     \
@@ -198,18 +200,19 @@ int main(int argc, char** argv) {
   CHECK(hipEventElapsedTime(&ms, e0, e1));
   const double us_call = 1000.0 * ms / (reps * R);
 
-  // one traced rotation: launch r writes its stamps to trace + r * waves * 16
+  // one traced rotation, launched back to back right behind untraced ones
+  // (the steady state of the timed loop): launch r writes its stamps to
+  // trace + r * waves * 16
   const size_t per_launch = static_cast<size_t>(waves) * 16;
   unsigned long long* trace = device_alloc<unsigned long long>(per_launch * R);
   CHECK(hipMemset(trace, 0, per_launch * R * sizeof(unsigned long long)));
-  for (int r = 0; r < R; ++r) {
-    unsigned long long* p = trace + r * per_launch;
-    CHECK(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &p, sizeof(p)));
-    CHECK(uqm::launch_moe_decode_fused(enc, inst[r], 0));
-    CHECK(hipDeviceSynchronize());
-  }
-  unsigned long long* none = nullptr;
-  CHECK(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &none, sizeof(none)));
+  CHECK(hipDeviceSynchronize());
+  std::vector<uqm::FusedArgs> traced(inst);
+  for (int r = 0; r < R; ++r) traced[r].trace = trace + r * per_launch;
+  for (int w = 0; w < 2; ++w)
+    for (int r = 0; r < R; ++r) CHECK(uqm::launch_moe_decode_fused(enc, inst[r], 0));
+  for (int r = 0; r < R; ++r) CHECK(uqm::launch_moe_decode_fused(enc, traced[r], 0));
+  CHECK(hipDeviceSynchronize());
   std::vector<unsigned long long> host(per_launch * R);
   CHECK(hipMemcpy(host.data(), trace, host.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost));
   uint32_t err = 0;
@@ -221,8 +224,24 @@ int main(int argc, char** argv) {
   printf("{\"config\": \"%s\", \"instances\": %d, \"reps\": %d, \"cus\": %d, \"us_per_call\": %.3f, "
          "\"algorithmic_bytes_per_call\": %zu, \"tb_per_s\": %.3f, \"error_word\": %u, \"clock_khz\": %d}\n",
          config, R, reps, cus, us_call, bytes_per_call, bytes_per_call / us_call / 1e6, err, khz);
+  {  // launch-to-launch period and span (last wave's last stamp) of the traced launches
+    std::vector<double> t0s;
+    double span = 0.0;
+    for (int r = 0; r < R; ++r) {
+      const unsigned long long* t = host.data() + r * per_launch;
+      unsigned long long a0 = ~0ull, a9 = 0;
+      for (int w = 0; w < waves; ++w) {
+        if (t[w * 16] != 0) a0 = std::min(a0, t[w * 16]);
+        for (int p = 0; p < 16; ++p) a9 = std::max(a9, t[w * 16 + p]);
+      }
+      t0s.push_back(a0 * tick_us);
+      span += (a9 - a0) * tick_us;
+    }
+    printf("traced launches back to back: mean start-to-start %.2f us, mean span (first entry to last stamp) %.2f us\n",
+           R > 1 ? (t0s.back() - t0s.front()) / (R - 1) : 0.0, span / R);
+  }
   printf("point  waves      min_us  median_us   max_us\n");
-  for (int p = 0; p < 10; ++p) {
+  for (int p = 0; p < 16; ++p) {
     for (int kind = 0; kind < 2; ++kind) {  // 0 streaming waves, 1 control waves
       double acc[3] = {0, 0, 0};
       int used = 0;

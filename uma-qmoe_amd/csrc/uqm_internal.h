@@ -183,6 +183,9 @@ struct FusedArgs {
   // ids [k] and bf16 routing weights [k]; NULL: the kernel routes itself.
   const int64_t* routes_in;
   const uint16_t* weights_in;
+  // Per-wave phase stamps of a timing harness that defines the kernel's trace
+  // hooks (csrc/timeline/fused_timeline.hip); NULL and unused in the library.
+  unsigned long long* trace;
 };
 
 // Returns >= 0 when a compiled instantiation covers (encoding, H, I, Is, k, E).
