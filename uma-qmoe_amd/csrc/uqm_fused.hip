@@ -78,14 +78,16 @@ constexpr int kWaves = 8;                  // streaming waves per workgroup
 constexpr int kThreads = (kWaves + 1) * 64;  // + the control wave
 constexpr int kLdsHeader = 256;            // flags, routes, weights, shared gate (16-byte aligned)
 constexpr uint16_t kBf16NaN = 0x7FC0;      // poison of products and outputs after an expired wait
-constexpr int kPollSleep = 40;             // s_sleep units (64 clocks) between router logit polls
-constexpr int kPollDelay = 64;             // s_sleep units before the first poll (the logits cannot be
-                                           // in sooner; fewer polls leave more bandwidth to phase A)
-// Without a shared expert nothing streams while the routes are pending (every
-// streaming wave waits for them), so the polls go out sooner and closer:
-// c1 17.3 vs 18.5 us per call, with one load per poll.
-constexpr int kPollSleepRoutedOnly = 20;
-constexpr int kPollDelayRoutedOnly = 24;
+// s_sleep units (64 clocks; s_sleep takes at most 127) before the first logit
+// poll with a shared expert: one poll is in flight at a time and each is
+// re-issued as soon as it returns incomplete (c2: 20.8-20.9 us per launch
+// back to back with a first delay of 96-127, 21.1 with 160, 21.4 with 192,
+// 22.1 with 40; three polls ~1 us apart from 64: 21.2-21.9)
+constexpr int kPollDelay = 104;
+// The same without a shared expert, where nothing streams while the routes
+// are pending (c1: 15.7 us per launch back to back with a first delay of 40,
+// 16.2 with 64, 16.7 with 12-24; three polls 20 apart from 24: 17.9-18.1).
+constexpr int kPollDelayRoutedOnly = 40;
 constexpr int kRouterHeadStart = 12;       // s_sleep units the streaming waves of router workgroups yield
 enum { kNormNone = 0, kNormUnit = 1, kNormWeighted = 2 };  // input RMSNorm: none, weight ones, weight row
 #ifndef UQM_FUSED_CTRL_PRIO
@@ -525,16 +527,17 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     }
     const uint32_t epoch = next_epoch(last_epoch);
     UQM_FUSED_TRACE(1);
-    // Every logit, once all its producers have published it. Three polls are
-    // kept in flight, ~1 us apart, so a late producer is seen one spacing (not
-    // one round trip) after it publishes; every poll issues the same loads
-    // (lanes past the end re-read the last word), which keeps the compiler's
-    // waits for the oldest poll exact. (All 256 control waves poll the same
-    // few lines: polling more often measurably slows the streaming phases.)
+    // Every logit, once all its producers have published it: one poll in
+    // flight, re-issued as soon as it comes back incomplete. (With several
+    // polls in flight, the one that finds every logit is followed by a wait
+    // for the later ones: the compiler reuses their registers for what comes
+    // next, and a register with a load outstanding waits for it first, up
+    // to a round trip.) Every poll issues the same loads (lanes past the end
+    // re-read the last word).
     float lv[LPL];
     bool bad = false;
     if constexpr (kShared) {
-      uint64_t pa[LPL], pb[LPL], pc[LPL];
+      uint64_t pa[LPL];
       auto poll = [&](uint64_t (&t)[LPL]) {
 #pragma unroll
         for (int j = 0; j < LPL; ++j) t[j] = co_load(a.lgt + min(lane + 64 * j, nrow - 1));
@@ -551,10 +554,6 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
       };
       __builtin_amdgcn_s_sleep(kPollDelay);
       poll(pa);
-      __builtin_amdgcn_s_sleep(kPollSleep);
-      poll(pb);
-      __builtin_amdgcn_s_sleep(kPollSleep);
-      poll(pc);
       for (;;) {
         if (!force_expiry && ready(pa)) {
           take(pa);
@@ -567,29 +566,15 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
           break;
         }
         poll(pa);
-        __builtin_amdgcn_s_sleep(kPollSleep);
-        if (ready(pb)) {
-          take(pb);
-          break;
-        }
-        poll(pb);
-        __builtin_amdgcn_s_sleep(kPollSleep);
-        if (ready(pc)) {
-          take(pc);
-          break;
-        }
-        poll(pc);
-        __builtin_amdgcn_s_sleep(kPollSleep);
       }
     } else {
-      // Without a shared expert nothing streams while the routes are
-      // pending, so the polls go sooner and closer: one load per lane when
-      // the rows fit in one (E <= 64), else LPL. (Written separately from the
-      // shared-expert case above: folding both into one routine changed the
-      // c2 kernel's code and cost it 0.4 us per call.)
+      // Without a shared expert: one load per lane when the rows fit in one
+      // (E <= 64), else LPL. (Written separately from the shared-expert case
+      // above: folding both into one routine changed the c2 kernel's code and
+      // cost it 0.4 us per call.)
       auto poll_logits = [&](auto loads) {
         constexpr int L = decltype(loads)::value;
-        uint64_t pa[L], pb[L], pc[L];
+        uint64_t pa[L];
         auto poll = [&](uint64_t (&t)[L]) {
 #pragma unroll
           for (int j = 0; j < L; ++j) t[j] = co_load(a.lgt + min(lane + 64 * j, nrow - 1));
@@ -606,10 +591,6 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
         };
         __builtin_amdgcn_s_sleep(kPollDelayRoutedOnly);
         poll(pa);
-        __builtin_amdgcn_s_sleep(kPollSleepRoutedOnly);
-        poll(pb);
-        __builtin_amdgcn_s_sleep(kPollSleepRoutedOnly);
-        poll(pc);
         for (;;) {
           if (!force_expiry && ready(pa)) {
             take(pa);
@@ -622,19 +603,6 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
             break;
           }
           poll(pa);
-          __builtin_amdgcn_s_sleep(kPollSleepRoutedOnly);
-          if (ready(pb)) {
-            take(pb);
-            break;
-          }
-          poll(pb);
-          __builtin_amdgcn_s_sleep(kPollSleepRoutedOnly);
-          if (ready(pc)) {
-            take(pc);
-            break;
-          }
-          poll(pc);
-          __builtin_amdgcn_s_sleep(kPollSleepRoutedOnly);
         }
       };
       if (nrow <= 64)
