@@ -259,6 +259,13 @@ __device__ __forceinline__ uint32_t bf16_key(uint16_t u) {
   if (u == 0x8000u) u = 0;
   return (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
 }
+// bf16_key of the bf16 bits u (low 16 bits) with selects only, no branches:
+// the same key for every value (any NaN pattern maps to 0xFFFF).
+__device__ __forceinline__ uint32_t bf16_key_select(uint32_t u) {
+  const uint32_t mag = u & 0x7FFFu;
+  const uint32_t k = ((u & 0x8000u) != 0u && mag != 0u) ? 0x7FFFu - mag : 0x8000u | mag;
+  return mag > 0x7F80u ? 0xFFFFu : k;
+}
 __device__ __forceinline__ float bf16_of_key(uint32_t key) {
   const uint32_t u = (key & 0x8000u) ? (key & 0x7FFFu) : (~key & 0xFFFFu);
   return bf16_to_f32(static_cast<uint16_t>(u));

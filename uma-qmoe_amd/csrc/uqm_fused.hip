@@ -464,10 +464,12 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
     // when it shares a SIMD with streaming waves.
     __builtin_amdgcn_s_setprio(UQM_FUSED_CTRL_PRIO);
     // After the routes are in LDS: the workgroup's barriers, the routed
-    // fragments, and the epoch advanced for the next launch.
-    auto finish_control = [&](uint32_t epoch) {
+    // fragments, and the epoch advanced for the next launch. `late` runs
+    // while the streaming waves issue their phase-B loads.
+    auto finish_control = [&](uint32_t epoch, auto late) {
       UQM_FUSED_TRACE(3);
       lds_barrier();  // routes ready
+      late();
       lds_barrier();  // routed gate/up rows issued
       lds_barrier();  // shared products staged
       lds_barrier();  // routed products staged
@@ -498,7 +500,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
         *l_bad = 0;
         *l_stale = 0;
       }
-      finish_control(next_epoch(last_epoch));
+      finish_control(next_epoch(last_epoch), [] {});
       return;
     }
     // Activation, epoch and router row loads go out together: one round trip.
@@ -611,24 +613,16 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
         poll_logits(std::integral_constant<int, LPL>{});
     }
     UQM_FUSED_TRACE(2);
-    // FP32 softmax statistics over the E expert logits.
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < LPL; ++j)
-      if (lane + 64 * j < E) mx = fmaxf(mx, lv[j]);
-    mx = wave_max(mx);
-    float se = 0.f;
-#pragma unroll
-    for (int j = 0; j < LPL; ++j)
-      if (lane + 64 * j < E) se += __expf(lv[j] - mx);
-    se = wave_sum(se);
     // Top-k by k rounds of a wave max over (value key, 0xFFFF - id): the
-    // largest logit wins, equal logits go to the lower expert id.
+    // largest logit wins, equal logits go to the lower expert id, NaN first
+    // (as in a descending sort). The logits are bf16 values, so a key comes
+    // straight from their upper 16 bits, without branches.
     uint32_t key[LPL];
 #pragma unroll
     for (int j = 0; j < LPL; ++j) {
       const int e = lane + 64 * j;
-      key[j] = e < E ? (bf16_key(f32_to_bf16(lv[j])) << 16) | static_cast<uint32_t>(0xFFFF - e) : 0u;
+      const uint32_t kv = (bf16_key_select(__float_as_uint(lv[j]) >> 16) << 16) | static_cast<uint32_t>(0xFFFF - e);
+      key[j] = e < E ? kv : 0u;
     }
     int route_e = 0;
     float route_l = 0.f;
@@ -645,37 +639,58 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
         route_l = bf16_of_key(m >> 16);
       }
     }
-    float p = lane < k ? __expf(route_l - mx) / se : 0.f;
-    if (a.norm) p = p / wave_sum(p);
-    const uint16_t wb = bad ? kBf16NaN : f32_to_bf16(p);
-    if (lane < k) {
-      l_route[lane] = route_e;
-      l_w[lane] = bf16_to_f32(wb);
-    }
+    if (lane < k) l_route[lane] = route_e;
     if (lane == 0) {
       *l_bad = bad ? 1 : 0;
       *l_stale = 0;
     }
-    if constexpr (kShared) {
-      float le = 0.f;
+    // FP32 softmax over the E expert logits at the k selected ones, the
+    // shared gate, and workgroup 0's outputs: only phase C reads them.
+    // Without a shared expert they are computed while the streaming waves
+    // issue their phase-B loads (c1 15.2 vs 15.5 us per call); with one,
+    // before the routes go out (there the later placement measured slower,
+    // 20.41 vs 20.28 us).
+    auto weights = [&]() {
+      float mx = -INFINITY;
 #pragma unroll
       for (int j = 0; j < LPL; ++j)
-        if (j == (E >> 6)) le = lv[j];
-      const float gl = lane_value(le, E & 63);
-      if (lane == 0) *l_sg = round_bf16(sigmoidf_(gl));
-    }
-    if (b == 0) {
-      if (lane < k) {
-        if (a.weights_out != nullptr) a.weights_out[lane] = wb;
-        if (a.indices_out != nullptr) a.indices_out[lane] = bad ? -1 : route_e;
-      }
-      if (a.logits_out != nullptr) {
+        if (lane + 64 * j < E) mx = fmaxf(mx, lv[j]);
+      mx = wave_max(mx);
+      float se = 0.f;
+#pragma unroll
+      for (int j = 0; j < LPL; ++j)
+        if (lane + 64 * j < E) se += __expf(lv[j] - mx);
+      se = wave_sum(se);
+      float p = lane < k ? __expf(route_l - mx) / se : 0.f;
+      if (a.norm) p = p / wave_sum(p);
+      const uint16_t wb = bad ? kBf16NaN : f32_to_bf16(p);
+      if (lane < k) l_w[lane] = bf16_to_f32(wb);
+      if constexpr (kShared) {
+        float le = 0.f;
 #pragma unroll
         for (int j = 0; j < LPL; ++j)
-          if (lane + 64 * j < E) a.logits_out[lane + 64 * j] = f32_to_bf16(lv[j]);
+          if (j == (E >> 6)) le = lv[j];
+        const float gl = lane_value(le, E & 63);
+        if (lane == 0) *l_sg = round_bf16(sigmoidf_(gl));
       }
+      if (b == 0) {
+        if (lane < k) {
+          if (a.weights_out != nullptr) a.weights_out[lane] = wb;
+          if (a.indices_out != nullptr) a.indices_out[lane] = bad ? -1 : route_e;
+        }
+        if (a.logits_out != nullptr) {
+#pragma unroll
+          for (int j = 0; j < LPL; ++j)
+            if (lane + 64 * j < E) a.logits_out[lane + 64 * j] = f32_to_bf16(lv[j]);
+        }
+      }
+    };
+    if constexpr (kShared) {
+      weights();
+      finish_control(epoch, [] {});
+    } else {
+      finish_control(epoch, weights);
     }
-    finish_control(epoch);
     return;
   }
 
