@@ -61,6 +61,24 @@ def close(got, ref, what, rel=REL_L2, mx=MAX_ABS):
     assert m <= mx, f"{what}: max-abs {m}"
 
 
+def within_ulps(got, ref, what, ulps=2, rel=5e-3):
+    """Two HIP paths that sum the same FP32 products in different orders:
+    every bf16 output within `ulps` bf16 ulps of the other path's, rel-L2 <=
+    rel. The ulp is that of the larger magnitude (2^(e - 7) for |y| in
+    [2^e, 2^(e+1))), at least the ulp of the outputs' RMS: near zero the sums'
+    rounding error follows the size of their terms, not of the result."""
+    a, b = got.cpu().float(), ref.cpu().float()
+    r = om.rel_l2(a, b)
+    rms = b.pow(2).mean().sqrt().item()
+    mag = torch.maximum(a.abs(), b.abs()).clamp_min(max(rms, 2.0 ** -126))
+    ulp = torch.exp2(torch.floor(torch.log2(mag)) - 7)
+    worst = ((a - b).abs() / ulp).max().item()
+    print(f"  {what}: rel_l2={r:.3e} max_ulps={worst:.1f}", flush=True)
+    assert torch.isfinite(a).all(), what
+    assert r <= rel, f"{what}: rel-L2 {r}"
+    assert worst <= ulps, f"{what}: {worst} bf16 ulps"
+
+
 def routes(t, k, e, seed, hot=None, hot_share=0.0):
     g = torch.Generator().manual_seed(seed)
     idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(t)])
@@ -279,11 +297,12 @@ def test_qwen_block_batched_decode(mfma_on, t):
     close(out, out_g, f"c2 block mfma vs gemv t={t}", rel=5e-3, mx=1e-2)
 
 
-@pytest.mark.parametrize("t", [4, 32])
+@pytest.mark.parametrize("t", [4, 32, 160])
 def test_shared_expert_side_stream(mfma_on, t):
     """The shared expert forked onto the library's side stream (the default)
     gives the same bits as the in-order run on the caller's stream, eagerly and
-    replayed from a HIP graph (several replays, eager work in between)."""
+    replayed from a HIP graph (several replays, eager work in between). At 160
+    tokens the shared expert takes the dense kernel."""
     ext = mfma_on
     shape = syn.C2
     note(f"shared expert side stream t={t}")
@@ -314,6 +333,39 @@ def test_shared_expert_side_stream(mfma_on, t):
         del graph
     finally:
         ext.set_option(_native.UQM_OPT_OVERLAP_SHARED, 1)
+
+
+RAGGED = syn.MoEShape("dense_ragged", 1088, 8, 2, 256, 1344, encoding="bf16_le")
+
+
+@pytest.mark.parametrize("which,t", [("ragged", 128), ("ragged", 200), ("ragged", 300), ("c2", 200), ("c2", 384),
+                                     ("c2", 1000)])
+def test_dense_shared_expert(mfma_on, which, t):
+    """From 128 tokens the shared expert takes the dense kernel: 4-wave items
+    of 128 weight rows x 128 tokens, or 8-wave items of 256 tokens where they
+    take fewer rounds over the CUs. The ragged shape has partial 128-token
+    tiles, a hidden size of 1088 (the down projection's last 128-row block
+    half full) and 1344 shared rows (21 K stages in the down projection: no K
+    split); c2 at 200 tokens splits the down projection's K in four; at 384
+    tokens the gate/up takes 8-wave items (the second 256-token tile half
+    full); at 1000 tokens both projections take 8-wave items, the down
+    projection with its K split in four. Against the oracle on sampled tokens
+    (the last token always among them) and against the GEMV path on every
+    token."""
+    ext = mfma_on
+    shape = RAGGED if which == "ragged" else syn.C2
+    note(f"dense shared expert {which} t={t}")
+    layer = syn.build_experts(shape, device=DEV)
+    dense = syn.build_dense(shape, device=DEV)
+    x = syn.hidden_states(shape, t, seed=90 + t)
+    (out, logits, weights, indices), (out_g, *_rest) = both_paths(
+        ext, lambda: ext.moe_layer(layer, dense, x.to(DEV), shape.top_k))
+    within_ulps(out, out_g, f"dense shared {which} t={t} vs gemv")
+    pick = torch.randperm(t, generator=torch.Generator().manual_seed(t))[:12]
+    pick = torch.unique(torch.cat([pick, torch.tensor([t - 1])]))
+    ref, *_ = om.qwen_block(x[pick], layout_of(shape, dense_cpu(dense)), syn.DeviceLayerReader({0: layer}), 0,
+                            routes=(weights.cpu()[pick], indices.cpu()[pick]))
+    close(out.cpu()[pick], ref, f"dense shared {which} t={t} sampled tokens vs oracle")
 
 
 def test_c4_prefill_512_tokens(mfma_on):

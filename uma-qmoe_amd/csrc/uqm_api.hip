@@ -11,6 +11,7 @@
 #include <unordered_map>
 
 #include "../../include/uma_qmoe_hip.h"
+#include "uqm_dense.h"
 #include "uqm_internal.h"
 #include "uqm_route.h"
 
@@ -218,6 +219,12 @@ bool routed_uses_mfma(const uqm_expert_weights* w, int64_t T) {
 bool shared_uses_mfma(int64_t H, int64_t Is, int64_t T) {
   const int64_t min_t = g_opt_mfma_min_tokens.load(std::memory_order_relaxed);
   return min_t > 0 && T >= min_t && uqm::mfma_supported(UQM_BF16, Is, H, 0) && uqm::mfma_supported(UQM_BF16, H, Is, 0);
+}
+
+// The shared expert of calls with many tokens takes the dense kernel.
+bool shared_uses_dense(int64_t H, int64_t Is, int64_t T) {
+  return g_opt_mfma_min_tokens.load(std::memory_order_relaxed) > 0 && uqm::dense_supported(Is, H, T) &&
+         uqm::dense_supported(H, Is, T);
 }
 
 // Whether the GEMV path of the routed experts streams (uqm_stream.hip) rather
@@ -502,6 +509,39 @@ int run_shared(const uqm_layer_weights* layer, const uint16_t* x, int64_t T, int
   using namespace uqm;
   const int64_t Is = layer->shared_intermediate_size;
   *parts = 1;
+  if (shared_uses_dense(H, Is, T)) {
+    // Dense square tiles (uqm_dense.hip); beside the routing chain at 3/4 of
+    // the CUs, as the grouped kernel below.
+    const int cus = beside ? device_cus() * 3 / 4 : device_cus();
+    DenseArgs g{};
+    g.w[0] = static_cast<const uint16_t*>(layer->shared_gate);
+    g.w[1] = static_cast<const uint16_t*>(layer->shared_up);
+    g.x = x;
+    g.ldx = H;
+    g.rows = Is;
+    g.K = H;
+    g.T = T;
+    g.out = at<uint16_t>(ws, L.h_shared);
+    g.ldo = Is;
+    g.ksplit = 1;
+    const DensePlan pg = plan_dense(2, Is, H, T, cus, 1);
+    int rc = hip_check(launch_dense_mfma(2, g, pg.waves, cus, stream), "shared gate/up dense launch");
+    if (rc) return rc;
+    DenseArgs d{};
+    d.w[0] = static_cast<const uint16_t*>(layer->shared_down);
+    d.x = at<uint16_t>(ws, L.h_shared);
+    d.ldx = Is;
+    d.rows = H;
+    d.K = Is;
+    d.T = T;
+    d.out = at<float>(ws, L.y_shared);
+    d.ldo = H;
+    d.part_stride = T * H;
+    const DensePlan pd = plan_dense(1, H, Is, T, cus, kMaxSplit);
+    d.ksplit = pd.ksplit;
+    *parts = d.ksplit;
+    return hip_check(launch_dense_mfma(1, d, pd.waves, cus, stream), "shared down dense launch");
+  }
   if (shared_uses_mfma(H, Is, T)) {
     // Up to 32 tokens: 16-token tiles, so that the plan can split K over
     // waves (16-row items) and fill the grid; the second tile of a row block
