@@ -88,6 +88,13 @@ constexpr int kPollDelay = 104;
 // are pending (c1: 15.7 us per launch back to back with a first delay of 40,
 // 16.2 with 64, 16.7 with 12-24; three polls 20 apart from 24: 17.9-18.1).
 constexpr int kPollDelayRoutedOnly = 40;
+// Without a shared expert the routed products are staged right after a
+// wave's own phase B, while other CUs are still publishing theirs: a first
+// staging round that comes back incomplete costs a round trip. Waiting this
+// many s_sleep units first (the routed down rows already in flight) lets it
+// complete (c1 in bench.py: 14.66 vs 15.22 us per call; 8: 14.90, 16: 14.71,
+// 32: 14.76, 64: 15.55).
+constexpr int kProductDelayRoutedOnly = 24;
 constexpr int kRouterHeadStart = 12;       // s_sleep units the streaming waves of router workgroups yield
 enum { kNormNone = 0, kNormUnit = 1, kNormWeighted = 2 };  // input RMSNorm: none, weight ones, weight row
 #ifndef UQM_FUSED_CTRL_PRIO
@@ -1003,6 +1010,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(FusedArgs a)
       issue_cs(oa < ob ? oa : H - 1, colIS);
     if constexpr (kShared) stage_hs(vs);
   }
+  if constexpr (!kShared) __builtin_amdgcn_s_sleep(kProductDelayRoutedOnly);
   load_round(hr64, n2r, base0, vr);
   if constexpr (kSplit)
     issue_cs_range(oa < ob ? oa : H - 1, std::integral_constant<int, CSA>{}, std::integral_constant<int, CISX>{});
