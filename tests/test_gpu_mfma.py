@@ -278,6 +278,31 @@ def test_48_route_tiles(mfma_on):
     close(got, got_g, "48-route tiles mfma vs gemv", rel=5e-3, mx=1e-2)
 
 
+# K / 128 odd in both projections (H = 1152: 9 scale groups, I = 896: 7)
+ODD = syn.MoEShape("odd_k", 1152, 40, 4, 896)
+
+
+@pytest.mark.parametrize("t", [6, 32, 200, 400])
+def test_q4_odd_group_count(mfma_on, t):
+    """Q4 projections whose K holds an odd number of 128-element scale groups,
+    so the 16-route gate/up tiles cannot take two-group steps (K a multiple of
+    256; the MID shape's gate/up and the c2 block's at batch 16 and 32 take
+    them) and run one group per step. The planner takes (gate/up; down): t=6
+    64-row items (down with two K-split partials when the items are few); t=32
+    128-row items, 16-route tiles; t=200 32-route tiles; t=400 48-route tiles.
+    Against the oracle and the GEMV path."""
+    ext = mfma_on
+    note(f"mfma odd group count t={t}")
+    layer = syn.build_experts(ODD, seed=60 + t)
+    dl = to_dev(layer)
+    x = syn.hidden_states(ODD, t, seed=60 + t)
+    idx, w = routes(t, ODD.top_k, ODD.num_experts, 160 + t)
+    got, gemv = both_paths(ext, lambda: ext.moe_forward(dl, x.to(DEV), idx.to(DEV), w.to(DEV)))
+    ref = om.streaming_reference(x, idx, w, 0, syn.DeviceLayerReader({0: layer}), num_experts=ODD.num_experts)
+    close(got, ref, f"odd groups vs oracle t={t}")
+    close(got, gemv, f"odd groups mfma vs gemv t={t}", rel=5e-3, mx=1e-2)
+
+
 @pytest.mark.parametrize("t", [2, 16, 32])
 def test_qwen_block_batched_decode(mfma_on, t):
     """c2 shapes at batch 2, 16 and 32: router, routed Q4 experts and the BF16

@@ -36,6 +36,15 @@
 // sits at position q + 4 S) and XOR-swizzled by the token index, so the B
 // reads of all 64 lanes hit distinct banks (b_position).
 //
+// Q4 gate/up tiles of 16 routes also have a wide form (kQ4Wide): a step
+// covers two 128-element scale groups, 128 contiguous bytes of a row, and each
+// 1 KB weight load takes 8 rows x 128 B instead of 16 rows x 64 B. A lane then
+// fills the 16 bytes of one row segment (XOR-swizzled by the row so that the
+// MMA waves' A reads are free of bank conflicts) and an MMA lane reads two of
+// them, one per scale group. Loads of 128-byte row segments stream faster than
+// loads of 64-byte ones (device-wide, through LDS DMA: 6.0-6.2 vs 5.6-5.7
+// TB/s); the batch-32 gate/up kernel gains ~1.5 us of ~48.
+//
 // Work tiles come from the device-built tile list (expert, first route).
 #include <atomic>
 #include <type_traits>
@@ -49,6 +58,10 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) unsigned char lds_uchar_t;
 
+// Q4 weights with two scale groups per step (kernel template value only; the
+// weights are the same UQM_Q4 bytes)
+constexpr int kQ4Wide = 3;
+
 template <int ENC>
 struct MEnc;
 template <>
@@ -56,13 +69,23 @@ struct MEnc<kQ4> {
   static constexpr int kChunk = 128;      // K elements per step (one scale group)
   static constexpr int kLoads = 1;        // 16-byte slots per lane per step and A tile
   static constexpr int kChunkBytes = 64;  // bytes of one row's chunk
+  static constexpr int kBits = 4;         // bits per weight
   static constexpr float kBias = 136.0f;  // bf16(0x4300 | (nibble ^ 8)) = 136 + q
+};
+template <>
+struct MEnc<kQ4Wide> {
+  static constexpr int kChunk = 256;
+  static constexpr int kLoads = 2;
+  static constexpr int kChunkBytes = 128;
+  static constexpr int kBits = 4;
+  static constexpr float kBias = 136.0f;
 };
 template <>
 struct MEnc<kQ8> {
   static constexpr int kChunk = 128;
   static constexpr int kLoads = 2;
   static constexpr int kChunkBytes = 128;
+  static constexpr int kBits = 8;
   static constexpr float kBias = 128.0f;  // byte ^ 0x80 = q + 128
 };
 template <>
@@ -70,6 +93,7 @@ struct MEnc<kBF16> {
   static constexpr int kChunk = 64;
   static constexpr int kLoads = 2;
   static constexpr int kChunkBytes = 128;
+  static constexpr int kBits = 16;
   static constexpr float kBias = 0.0f;
 };
 
@@ -83,18 +107,18 @@ __device__ __forceinline__ uint32_t hi16_pair(float lo, float hi) {
 }
 
 // A operand (8 weights) of K-step S of a chunk from the lane's 16-byte slots.
-//   Q4: dword S of slot 0 = elements 32q+8S .. +7
-
+//   Q4: dword S%4 of slot S/4 = elements 128(S/4)+32q+8(S%4) .. +7 (one slot,
+//       S < 4, in the narrow form)
 //   Q8: slot S/2, dwords 2(S%2), 2(S%2)+1 = elements 64(S/2)+16q+8(S%2) .. +7
 //   BF16: slot S = elements 32S+8q .. +7
 template <int ENC, int S>
 __device__ __forceinline__ bf16x8_t a_frag(const uint4 (&v)[MEnc<ENC>::kLoads]) {
   u32x4_t o;
-  if constexpr (ENC == kQ4) {
+  if constexpr (ENC == kQ4 || ENC == kQ4Wide) {
     // pair d = (element 2d, element 2d + 1) = low and high nibble of byte d:
     // v_perm puts byte d of w at bits 0-7 and byte d of w >> 4 at bits 16-23,
     // then one masked xor/or (a single v_bitop3) makes both bf16 values
-    const uint32_t w = dw(v[0], S);
+    const uint32_t w = dw(v[S >> 2], S & 3);
     const uint32_t h = w >> 4;
     o.x = (perm(h, w, 0x0C040C00u) ^ 0x00080008u) & 0x000F000Fu | 0x43004300u;
     o.y = (perm(h, w, 0x0C050C01u) ^ 0x00080008u) & 0x000F000Fu | 0x43004300u;
@@ -120,18 +144,51 @@ __device__ __forceinline__ bf16x8_t a_frag(const uint4 (&v)[MEnc<ENC>::kLoads]) 
 // lane quadrant q, matching a_frag's order.
 template <int ENC>
 __device__ __forceinline__ int b_slot(int q, int S) {
-  if constexpr (ENC == kQ4) return 4 * q + S;
+  if constexpr (ENC == kQ4 || ENC == kQ4Wide) return 16 * (S >> 2) + 4 * q + (S & 3);
   else if constexpr (ENC == kQ8) return 8 * (S >> 1) + 2 * q + (S & 1);
   else return 4 * S + q;
 }
 
 // LDS position of that slot in a staged activation row: q + 4 S, XOR-ed with
-// the row's token index. Reads of one K-step then have q in the low two bits
-// of the position, which the gfx950 LDS serves without bank conflicts for all
-// 64 lanes; with q in bits 2-3 (the chunk order of a Q4 fragment) half of the
-// LDS cycles of the batch-32 Q4 kernels were bank-conflict stalls (rocprofv3
-// SQ_LDS_BANK_CONFLICT), and a probe of both patterns on their own confirms it.
-__device__ __forceinline__ int b_position(int q, int S, int row, int spr) { return (q + 4 * S) ^ (row & (spr - 1)); }
+// the row's token index (its low bits, up to 4). Reads of one K-step then have
+// q in the low two bits of the position, which the gfx950 LDS serves without
+// bank conflicts for all 64 lanes; with q in bits 2-3 (the chunk order of a Q4
+// fragment) half of the LDS cycles of the batch-32 Q4 kernels were
+// bank-conflict stalls (rocprofv3 SQ_LDS_BANK_CONFLICT), and a probe of both
+// patterns on their own confirms it.
+__device__ __forceinline__ int b_position(int q, int S, int row, int spr) {
+  return (q + 4 * S) ^ (row & ((spr < 16 ? spr : 16) - 1));
+}
+
+// Weight loads: load u of a 16-row A tile puts lane l's 16 bytes at LDS byte
+// 1024 u + 16 l of the tile. Row (within the tile) and byte (within the row's
+// chunk) lane l loads there:
+//   narrow: row l % 16, byte 16 (l / 16) + 64 u (16 rows x 64 B per load)
+//   Q4 wide: row 8 u + l / 8, 16-byte segment (l % 8) ^ ((row / 2) % 8)
+//            (8 rows x 128 B per load; the tile is row-major, 128 B per row)
+template <int ENC>
+__device__ __forceinline__ int a_load_row(int lane, int u) {
+  if constexpr (ENC == kQ4Wide) return 8 * u + (lane >> 3);
+  else return lane & 15;
+}
+template <int ENC>
+__device__ __forceinline__ int a_load_byte(int lane, int u) {
+  if constexpr (ENC == kQ4Wide) return 16 * ((lane & 7) ^ ((a_load_row<ENC>(lane, u) >> 1) & 7));
+  else return 16 * (lane >> 4) + 64 * u;
+}
+// LDS byte (within the tile) of the MMA lane's slot u: narrow, the 16 bytes
+// load u put there for this lane; Q4 wide, row l % 16's segment 4 u + l / 16
+// (scale group u), where the swizzle put it. Lanes l and l + 16 k read rows
+// l % 16 at distinct 16-byte bank groups.
+template <int ENC>
+__device__ __forceinline__ int a_read_off(int lane, int u) {
+  if constexpr (ENC == kQ4Wide) {
+    const int r = lane & 15;
+    return 128 * r + 16 * ((4 * u + (lane >> 4)) ^ ((r >> 1) & 7));
+  } else {
+    return 1024 * u + 16 * lane;
+  }
+}
 
 // s_waitcnt with only vmcnt limited (gfx9 encoding: vmcnt bits 3:0 and 15:14).
 template <int N>
@@ -171,6 +228,7 @@ struct MfmaCfg {
   static constexpr int CH = M::kChunk;
   static constexpr int L = M::kLoads;
   static constexpr int KS = CH / 32;  // MFMA K-steps per chunk
+  static constexpr int GPC = ENC == kQ4Wide ? 2 : 1;  // 128-element scale groups per step
   static constexpr int AT = NMAT;     // 16-row A tiles per MMA wave (gate and up, or one)
   static constexpr int WR = MW / KW;  // MMA waves along the rows
   static constexpr int NTOK = 16 * NB;
@@ -189,7 +247,9 @@ struct MfmaCfg {
   static constexpr int NL = (D - 2) * I_STEP > 63 ? 2 : 1;  // loader waves
   static constexpr int I_WAVE = I_STEP / NL;
   static constexpr int THREADS = 64 * (MW + NL);
-  static constexpr int SLOTS = 3;                      // item slots for the scales
+  // item slots for the scales: 2 for the wide Q4 gate/up tiles (40 KB steps),
+  // whose ring and three slots would not fit the LDS
+  static constexpr int SLOTS = ENC == kQ4Wide && NMAT == 2 ? 2 : 3;
   static constexpr int MAX_ITEMS = NTOK <= 32 ? 32 : 16;  // work items per workgroup
   static constexpr int META = 4 + NTOK;                // expert, first route, routes, row block, route ids
   static constexpr int RED_BYTES = KW > 1 ? (KW - 1) * WR * AT * NB * 4 * 64 * 4 : 0;
@@ -253,8 +313,8 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
   const int S = (c_end - c_begin + KW - 1) / KW;  // steps per item
   const int total = nit * S;
   const int G = kScaled ? static_cast<int>(a.K / a.group) : 0;  // scale groups per row
-  const int gdiv = kScaled ? static_cast<int>(a.group / CH) : 1;
-  const int64_t row_bytes = ENC == kQ4 ? a.K / 2 : (ENC == kQ8 ? a.K : 2 * a.K);
+  const int gdiv = kScaled ? static_cast<int>(a.group / 128) : 1;  // 128-element sub-chunks per scale group
+  const int64_t row_bytes = a.K * M::kBits / 8;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -297,9 +357,9 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
     // =========================== loader waves ===========================
     const int lw = NL == 1 ? 0 : wave - MW;
     constexpr int XW = C::X_INSTR / NL;  // activation loads of this wave per step
-    const uint8_t* wrow[AT];  // this lane's row in A tile ai of MMA wave 0 (chunk 0 of the item)
-    const uint8_t* xsrc[XW];  // this lane's activation row slot of each of its activation loads
-    int xkw[XW];              // K group of the chunk an activation load feeds
+    const uint8_t* wrow[AT][L];  // this lane's bytes of load u of A tile ai of MMA wave 0 (chunk 0 of the item)
+    const uint8_t* xsrc[XW];     // this lane's activation row slot of each of its activation loads
+    int xkw[XW];                 // K group of the chunk an activation load feeds
     int cur = -1;
     auto setup_item = [&](int i) {
       const int* m = meta + i * META;
@@ -308,16 +368,20 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
 #pragma unroll
       for (int ai = 0; ai < AT; ++ai) {
         const int mat = NMAT == 2 ? ai : 0;
-        int64_t row = row0 + (lane & 15);
-        if constexpr (WR == 1) {
-          // clamped padding rows and the appended tail row (router + shared-expert gate)
-          if (a.rows_valid > 0 && row >= a.rows_valid) row = a.rows_valid - 1;
-          if (mat == 0 && a.w_tail != nullptr && row >= a.tail_from) {
-            wrow[ai] = a.w_tail + (row - a.tail_from) * row_bytes + (lane >> 4) * 16;
-            continue;
+#pragma unroll
+        for (int u = 0; u < L; ++u) {
+          int64_t row = row0 + a_load_row<ENC>(lane, u);
+          const int byte = a_load_byte<ENC>(lane, u);
+          if constexpr (WR == 1) {
+            // clamped padding rows and the appended tail row (router + shared-expert gate)
+            if (a.rows_valid > 0 && row >= a.rows_valid) row = a.rows_valid - 1;
+            if (mat == 0 && a.w_tail != nullptr && row >= a.tail_from) {
+              wrow[ai][u] = a.w_tail + (row - a.tail_from) * row_bytes + byte;
+              continue;
+            }
           }
+          wrow[ai][u] = a.w[mat] + (static_cast<int64_t>(expert) * a.rows + row) * row_bytes + byte;
         }
-        wrow[ai] = a.w[mat] + (static_cast<int64_t>(expert) * a.rows + row) * row_bytes + (lane >> 4) * 16;
       }
 #pragma unroll
       for (int k = 0; k < XW; ++k) {
@@ -326,7 +390,7 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
         const int tok = r % NTOK;
         // this lane fills LDS position lane % SPR of row r: the slot whose
         // (q, S) b_position maps there
-        const int u = (lane % C::SPR) ^ (r & (C::SPR - 1));
+        const int u = (lane % C::SPR) ^ (r & ((C::SPR < 16 ? C::SPR : 16) - 1));
         const int slot = b_slot<ENC>(u & 3, u >> 2);
         const int route = m[4 + tok];
         xsrc[k] = reinterpret_cast<const uint8_t*>(a.x + static_cast<int64_t>(route / a.x_div) * a.ldx) + slot * 16;
@@ -366,8 +430,7 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
         const int ai = (ii / L) % AT;
         const int cw = ii / (L * AT);
         const int c = min(cb + cw / WR, c_end - 1);
-        dma16_to(wrow[ai] + ((cw % WR) * wave_rows + static_cast<int64_t>(c) * M::kChunkBytes + u * 64),
-                 buf + ii * 1024);
+        dma16_to(wrow[ai][u] + ((cw % WR) * wave_rows + static_cast<int64_t>(c) * M::kChunkBytes), buf + ii * 1024);
       }
 #pragma unroll
       for (int k = 0; k < XW; ++k) {
@@ -416,18 +479,18 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
       for (int ai = 0; ai < AT; ++ai)
 #pragma unroll
         for (int u = 0; u < L; ++u)
-          wv[ai][u] = *reinterpret_cast<const uint4*>(buf + ((wave * AT + ai) * L + u) * 1024 + lane * 16);
+          wv[ai][u] = *reinterpret_cast<const uint4*>(buf + (wave * AT + ai) * L * 1024 + a_read_off<ENC>(lane, u));
       const unsigned char* xb = buf + C::W_BYTES + (kw * NTOK + t16) * C::ROWB;
       f32x4_t d[AT][NB];
       f32x4_t xs[NB];
-      if constexpr (kScaled) {
+      auto clear = [&]() {
 #pragma unroll
         for (int ai = 0; ai < AT; ++ai)
 #pragma unroll
           for (int b = 0; b < NB; ++b) d[ai][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int b = 0; b < NB; ++b) xs[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      }
+      };
       auto kstep = [&](auto s_tag) {
         constexpr int S_ = decltype(s_tag)::value;
         const int slot = b_position(q, S_, t16, C::SPR);
@@ -451,17 +514,19 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
           }
         }
       };
-      kstep(std::integral_constant<int, 0>{});
-      kstep(std::integral_constant<int, 1>{});
-      if constexpr (KS > 2) {
-        kstep(std::integral_constant<int, 2>{});
-        kstep(std::integral_constant<int, 3>{});
-      }
-      if constexpr (kScaled) {
+      // one 128-element scale group h of the step: its four K-steps (sums
+      // in d, xs), then acc += scale * (d - bias * sum(x))
+      auto group = [&](auto h_tag) {
+        constexpr int H_ = decltype(h_tag)::value;
+        clear();
+        kstep(std::integral_constant<int, 4 * H_>{});
+        kstep(std::integral_constant<int, 4 * H_ + 1>{});
+        kstep(std::integral_constant<int, 4 * H_ + 2>{});
+        kstep(std::integral_constant<int, 4 * H_ + 3>{});
         float xsb[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) xsb[b] = M::kBias * xs[b][0];
-        const int grp = c / gdiv;
+        const int grp = (c * C::GPC + H_) / gdiv;
         const float* sc_item = scl + (i % SLOTS) * NMAT * WGR * G;
 #pragma unroll
         for (int ai = 0; ai < AT; ++ai) {
@@ -476,6 +541,17 @@ __global__ __launch_bounds__((MfmaCfg<ENC, NMAT, MW, NB, KW>::THREADS)) void exp
             acc[ai][b][2] = fmaf(s2, d[ai][b][2] - xsb[b], acc[ai][b][2]);
             acc[ai][b][3] = fmaf(s3, d[ai][b][3] - xsb[b], acc[ai][b][3]);
           }
+        }
+      };
+      if constexpr (kScaled) {
+        group(std::integral_constant<int, 0>{});
+        if constexpr (C::GPC > 1) group(std::integral_constant<int, 1>{});
+      } else {
+        kstep(std::integral_constant<int, 0>{});
+        kstep(std::integral_constant<int, 1>{});
+        if constexpr (KS > 2) {
+          kstep(std::integral_constant<int, 2>{});
+          kstep(std::integral_constant<int, 3>{});
         }
       }
     }
@@ -558,6 +634,19 @@ size_t lds_bytes_for(int64_t K, int64_t group) {
   return static_cast<size_t>(C::FIXED_LDS) + sizeof(float) * C::SLOTS * NMAT * G * C::WGR;
 }
 
+// The item's scale slot is rewritten SLOTS items later, when the loader issues
+// that item's first step, up to D - 1 steps ahead of the MMA waves: safe when
+// (SLOTS - 1) steps per item >= D - 1. And the ring, the slots and the
+// metadata must fit the LDS.
+template <int ENC, int NMAT, int MW, int NB, int KW>
+bool cfg_fits(const MfmaArgs& a) {
+  using C = MfmaCfg<ENC, NMAT, MW, NB, KW>;
+  const int nch = static_cast<int>(a.K / C::CH);
+  const int steps = (nch / (a.ksplit > 0 ? a.ksplit : 1)) / KW;
+  if ((C::SLOTS - 1) * steps + 1 < C::D) return false;
+  return lds_bytes_for<ENC, NMAT, MW, NB, KW>(a.K, a.group) <= 160 * 1024;
+}
+
 // Workgroups of one configuration that fit on a CU (cached per LDS size).
 template <int ENC, int NMAT, int MW, int NB, int KW, int MODE>
 int blocks_per_cu(size_t lds) {
@@ -579,11 +668,8 @@ hipError_t launch_cfg(const MfmaArgs& args, int cus, hipStream_t stream) {
   using C = MfmaCfg<ENC, NMAT, MW, NB, KW>;
   MfmaArgs a = args;
   a.row_blocks = static_cast<int32_t>(a.rows / C::WGR);
-  const int nch = static_cast<int>(a.K / C::CH);
-  const int steps = (nch / (a.ksplit > 0 ? a.ksplit : 1)) / KW;
-  if (2 * steps + 1 < C::D) return hipErrorInvalidValue;  // scale slots would be reused too early
+  if (!cfg_fits<ENC, NMAT, MW, NB, KW>(a)) return hipErrorInvalidValue;
   const size_t lds = lds_bytes_for<ENC, NMAT, MW, NB, KW>(a.K, a.group);
-  if (lds > 160 * 1024) return hipErrorInvalidValue;
   constexpr int MODE = NMAT == 2 ? kModeSilu : kModeF32;
   auto kernel = expert_mfma_kernel<ENC, NMAT, MW, NB, KW, MODE>;
   if (lds > 64 * 1024) {
@@ -635,6 +721,24 @@ hipError_t launch_enc(int nmat, const MfmaArgs& a, int nb, int kw, int mw, int c
   return launch_nb<ENC, 1, 4, 1>(a, nb, cus, stream);
 }
 
+// Q4 gate/up tiles of 16 routes on the wide form (K-steps of two scale
+// groups, 8 rows x 128 B per weight load) when K is a multiple of 256 and the
+// ring and scales fit the LDS (K up to ~2400 at 128-element groups). Returns
+// hipErrorNotSupported when the call takes the narrow form. Measured against
+// the narrow form and kept narrow: down tiles (c4 171.3 vs 167.0 us per call,
+// c5 109.4 vs 97.9 with one workgroup per CU instead of two, batch 32 +1 us
+// with K = 1408, whose odd group count left one step half used) and wider
+// gate/up tiles (their rings do not fit).
+hipError_t launch_q4_wide(int nmat, const MfmaArgs& a, int nb, int kw, int mw, int cus, hipStream_t stream) {
+  if (nmat != 2 || nb != 1 || kw != 1 || a.group % 128 != 0 || a.K % 256 != 0) return hipErrorNotSupported;
+  if (mw == 8) {
+    if (!cfg_fits<kQ4Wide, 2, 8, 1, 1>(a)) return hipErrorNotSupported;
+    return launch_cfg<kQ4Wide, 2, 8, 1, 1>(a, cus, stream);
+  }
+  if (!cfg_fits<kQ4Wide, 2, 4, 1, 1>(a)) return hipErrorNotSupported;
+  return launch_cfg<kQ4Wide, 2, 4, 1, 1>(a, cus, stream);
+}
+
 }  // namespace
 
 bool mfma_supported(int enc, int64_t rows, int64_t K, int64_t group) {
@@ -658,6 +762,10 @@ hipError_t launch_expert_mfma(int enc, int nmat, const MfmaArgs& args, int nb, i
   if (enc != kBF16) a.scales_per_expert = (a.rows * a.K + a.group - 1) / a.group;
   if (a.tile_bound <= 0) return hipSuccess;
   if (cus < 8) cus = 8;
+  if (enc == kQ4) {
+    const hipError_t e = launch_q4_wide(nmat, a, nb, kw, mw, cus, stream);
+    if (e != hipErrorNotSupported) return e;
+  }
   if (enc == kQ4) return launch_enc<kQ4>(nmat, a, nb, kw, mw, cus, stream);
   if (enc == kQ8) return launch_enc<kQ8>(nmat, a, nb, kw, mw, cus, stream);
   return launch_enc<kBF16>(nmat, a, nb, kw, mw, cus, stream);
