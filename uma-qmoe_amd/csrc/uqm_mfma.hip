@@ -700,8 +700,11 @@ hipError_t launch_nb(const MfmaArgs& a, int nb, int cus, hipStream_t stream) {
     }
     if constexpr (MW == 4) {
       if (nb == 3) return hipErrorInvalidValue;
-      if (nb <= 4 || ENC != kBF16) return launch_cfg<ENC, NMAT, MW, 4, KW>(a, cus, stream);
-      if constexpr (ENC == kBF16) return launch_cfg<ENC, NMAT, MW, 8, KW>(a, cus, stream);
+      if (nb <= 4) return launch_cfg<ENC, NMAT, MW, 4, KW>(a, cus, stream);
+      // 128-route tiles exist for BF16 only (a smaller kernel tile would drop routes)
+      if constexpr (ENC == kBF16) {
+        if (nb <= 8) return launch_cfg<ENC, NMAT, MW, 8, KW>(a, cus, stream);
+      }
     }
   }
   return hipErrorInvalidValue;
