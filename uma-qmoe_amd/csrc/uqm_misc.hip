@@ -14,43 +14,89 @@
 
 namespace uqm {
 
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, int y_parts, int64_t y_stride,
+// The P FP32 partials of a row segment (loads only) and their sum in order.
+template <int P>
+__device__ __forceinline__ void load_parts(const float* __restrict__ base, int64_t stride, float4 (&u)[P]) {
+#pragma unroll
+  for (int p = 0; p < P; ++p) u[p] = *reinterpret_cast<const float4*>(base + p * stride);
+}
+template <int P>
+__device__ __forceinline__ float4 add_parts(const float4 (&u)[P]) {
+  float4 v = u[0];
+#pragma unroll
+  for (int p = 1; p < P; ++p) {
+    v.x += u[p].x;
+    v.y += u[p].y;
+    v.z += u[p].z;
+    v.w += u[p].w;
+  }
+  return v;
+}
+
+// One thread: 4 outputs of one token. YP routed and SP shared-expert FP32
+// partials (SP = 0: no shared expert). The loads of the first 4 route slots
+// (route id, weight, the partials of its row) and of the shared expert are
+// issued before any is used, so for k <= 4 the thread waits about one memory
+// round trip instead of one per slot and partial (each further group of 4
+// slots adds one); the row of a dropped route is read (it lies in the
+// workspace) and discarded. The arithmetic is the slot-order FMA chain of the
+// partials' sums, then the shared term.
+template <int YP, int SP>
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, int64_t y_stride,
                                                       const uint16_t* __restrict__ w,
                                                       const int64_t* __restrict__ idx, int64_t k, int64_t E,
-                                                      int64_t H, const float* __restrict__ ys, int ys_parts,
-                                                      int64_t ys_stride, const float* __restrict__ sg,
-                                                      uint16_t* __restrict__ out) {
+                                                      int64_t H, const float* __restrict__ ys, int64_t ys_stride,
+                                                      const float* __restrict__ sg, uint16_t* __restrict__ out) {
+  constexpr int kSlots = 4;
   const int64_t t = blockIdx.y;
   const int64_t o = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   if (o >= H) return;
+  float4 u[kSlots][YP];
+  float ws[kSlots];
+  bool live[kSlots];
+  auto load_group = [&](int64_t s0) {
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      const bool in = s0 + j < k;
+      const int64_t slot = t * k + (in ? s0 + j : s0);
+      const int64_t e = idx[slot];
+      live[j] = in && e >= 0 && e < E;
+      ws[j] = bf16_to_f32(w[slot]);
+      load_parts<YP>(y + slot * H + o, y_stride, u[j]);
+    }
+  };
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int64_t s = 0; s < k; ++s) {
-    const int64_t e = idx[t * k + s];
-    if (e < 0 || e >= E) continue;
-    const float ws = bf16_to_f32(w[t * k + s]);
-    float4 v = *reinterpret_cast<const float4*>(y + (t * k + s) * H + o);
-    for (int p = 1; p < y_parts; ++p) {
-      const float4 u = *reinterpret_cast<const float4*>(y + p * y_stride + (t * k + s) * H + o);
-      v.x += u.x;
-      v.y += u.y;
-      v.z += u.z;
-      v.w += u.w;
+  // a dropped slot keeps acc (a select, not a branch, so that the route ids
+  // load with everything else)
+  auto add_group = [&]() {
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      const float4 v = add_parts<YP>(u[j]);
+      const float4 f = make_float4(fmaf(ws[j], v.x, acc.x), fmaf(ws[j], v.y, acc.y), fmaf(ws[j], v.z, acc.z),
+                                   fmaf(ws[j], v.w, acc.w));
+      acc.x = live[j] ? f.x : acc.x;
+      acc.y = live[j] ? f.y : acc.y;
+      acc.z = live[j] ? f.z : acc.z;
+      acc.w = live[j] ? f.w : acc.w;
     }
-    acc.x = fmaf(ws, v.x, acc.x);
-    acc.y = fmaf(ws, v.y, acc.y);
-    acc.z = fmaf(ws, v.z, acc.z);
-    acc.w = fmaf(ws, v.w, acc.w);
+  };
+  load_group(0);
+  float4 su[SP > 0 ? SP : 1];
+  float g = 0.f;
+  if constexpr (SP > 0) {
+    g = sg[t];
+    load_parts<SP>(ys + t * H + o, ys_stride, su);
   }
-  if (ys != nullptr) {
-    const float g = sg[t];
-    float4 v = *reinterpret_cast<const float4*>(ys + t * H + o);
-    for (int p = 1; p < ys_parts; ++p) {
-      const float4 u = *reinterpret_cast<const float4*>(ys + p * ys_stride + t * H + o);
-      v.x += u.x;
-      v.y += u.y;
-      v.z += u.z;
-      v.w += u.w;
-    }
+  // keep the scheduler from moving the first group's arithmetic between its loads
+  __builtin_amdgcn_sched_barrier(0);
+  add_group();
+  for (int64_t s0 = kSlots; s0 < k; s0 += kSlots) {
+    load_group(s0);
+    __builtin_amdgcn_sched_barrier(0);
+    add_group();
+  }
+  if constexpr (SP > 0) {
+    const float4 v = add_parts<SP>(su);
     acc.x = fmaf(g, v.x, acc.x);
     acc.y = fmaf(g, v.y, acc.y);
     acc.z = fmaf(g, v.z, acc.z);
@@ -61,14 +107,57 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   *reinterpret_cast<uint2*>(out + t * H + o) = make_uint2(lo, hi);
 }
 
+namespace {
+
+struct CombineLaunch {
+  const float* y;
+  int64_t y_stride;
+  const uint16_t* weights;
+  const int64_t* indices;
+  int64_t T, k, E, H;
+  const float* ys;
+  int64_t ys_stride;
+  const float* sg;
+  uint16_t* out;
+  hipStream_t stream;
+};
+
+template <int YP, int SP>
+hipError_t launch_parts(const CombineLaunch& c) {
+  const dim3 grid(static_cast<unsigned>((c.H / 4 + 255) / 256), static_cast<unsigned>(c.T));
+  hipLaunchKernelGGL((combine_kernel<YP, SP>), grid, dim3(256), 0, c.stream, c.y, c.y_stride, c.weights, c.indices,
+                     c.k, c.E, c.H, c.ys, c.ys_stride, c.sg, c.out);
+  return hipGetLastError();
+}
+
+template <int YP>
+hipError_t launch_shared_parts(int sp, const CombineLaunch& c) {
+  switch (sp) {
+    case 0: return launch_parts<YP, 0>(c);
+    case 1: return launch_parts<YP, 1>(c);
+    case 2: return launch_parts<YP, 2>(c);
+    case 3: return launch_parts<YP, 3>(c);
+    case 4: return launch_parts<YP, 4>(c);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+// At most 4 K-split partials of each projection (the workspace holds 4).
 hipError_t launch_combine(const float* y, int y_parts, int64_t y_stride, const uint16_t* weights,
                           const int64_t* indices, int64_t T, int64_t k, int64_t E, int64_t H, const float* ys,
                           int ys_parts, int64_t ys_stride, const float* sg, uint16_t* out, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((H / 4 + 255) / 256), static_cast<unsigned>(T));
-  hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, stream, y, y_parts, y_stride, weights, indices, k, E, H,
-                     ys, ys_parts, ys_stride, sg, out);
-  return hipGetLastError();
+  const CombineLaunch c{y, y_stride, weights, indices, T, k, E, H, ys, ys_stride, sg, out, stream};
+  const int sp = ys == nullptr ? 0 : ys_parts;
+  switch (y_parts) {
+    case 1: return launch_shared_parts<1>(sp, c);
+    case 2: return launch_shared_parts<2>(sp, c);
+    case 3: return launch_shared_parts<3>(sp, c);
+    case 4: return launch_shared_parts<4>(sp, c);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, int64_t H,
