@@ -43,7 +43,7 @@
 // MMA waves' A reads are free of bank conflicts) and an MMA lane reads two of
 // them, one per scale group. Loads of 128-byte row segments stream faster than
 // loads of 64-byte ones (device-wide, through LDS DMA: 6.0-6.2 vs 5.6-5.7
-// TB/s); the batch-32 gate/up kernel gains ~1.5 us of ~48.
+// TB/s); the batch-32 gate/up kernel takes 45.5 vs 48.6 us (kernel trace).
 //
 // Work tiles come from the device-built tile list (expert, first route).
 #include <atomic>
