@@ -941,13 +941,10 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
       side_lock = std::unique_lock<std::mutex>(g_side_mu);
       side = side_stream(s);
     }
-    if (side != nullptr) {
-      if ((rc = hip_check(hipEventRecord(side->fork, s), "fork record")) ||
-          (rc = hip_check(hipStreamWaitEvent(side->stream, side->fork, 0), "fork wait")))
-        return rc;
-      join_on_exit.side = side;
-      if ((rc = run_shared(layer, x, tokens, H, L, workspace, &ys_parts, true, side->stream))) return rc;
-    }
+    // the fork point: the shared expert reads only the input, so it waits for
+    // nothing the routing chain does; its launches follow the routing chain's
+    // (below)
+    if (side != nullptr && (rc = hip_check(hipEventRecord(side->fork, s), "fork record"))) return rc;
   }
   // 1-2. router logits (+ shared-gate logit in column E), top-k
   uint16_t* wout = routing_weights != nullptr ? static_cast<uint16_t*>(routing_weights) : at<uint16_t>(workspace, L.weights);
@@ -1006,6 +1003,17 @@ int moe_layer_impl(const uqm_layer_weights* layer, const void* hidden, int64_t t
       (rc = hip_check(launch_route_permute(rt.route_expert, nullptr, tokens * k, E, rt, nullptr, nullptr, tile_tokens, s),
                       "permute launch")))
     return rc;
+  // The shared expert on the side stream, launched after the router and the
+  // top-k but dependent only on the fork: a HIP graph replay dispatches the
+  // nodes in this order, so the router's small grid goes out before the shared
+  // expert's persistent grids instead of ~5.6 us behind them (graph replay:
+  // batch 32 101.9-102.1 vs 102.9-103.2 us per call, T = 16 82.0-82.1 vs
+  // 88.6-88.7, c4 164.4-164.6 vs 167.6-167.7).
+  if (side != nullptr) {
+    if ((rc = hip_check(hipStreamWaitEvent(side->stream, side->fork, 0), "fork wait"))) return rc;
+    join_on_exit.side = side;
+    if ((rc = run_shared(layer, x, tokens, H, L, workspace, &ys_parts, true, side->stream))) return rc;
+  }
   // 3. routed experts
   int yr_parts = 1;
   if ((rc = run_routed(w, x, tokens, k, L, workspace, tile_tokens, &yr_parts, s))) return rc;
