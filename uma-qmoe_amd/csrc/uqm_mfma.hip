@@ -242,8 +242,14 @@ struct MfmaCfg {
   static constexpr int X_INSTR = X_BYTES / 1024;
   static constexpr int I_STEP = W_INSTR + X_INSTR;
   // ring depth: 48-route gate/up tiles (28 KB steps) keep 3 buffers so that
-  // the ring, three scale slots and the metadata fit the 160 KB of LDS
-  static constexpr int D = BUF <= 12 * 1024 ? 6 : (BUF <= 24 * 1024 || (BUF <= 32 * 1024 && NB != 3) ? 4 : 3);
+  // the ring, three scale slots and the metadata fit the 160 KB of LDS; the
+  // Q4 down projection's 16-route tiles (12 KB steps) keep 4, so that two
+  // workgroups (two loader waves) share a CU (batch 32 100.6-100.8 vs
+  // 102.3-102.5 us per call with 6, T = 16 80.0-80.3 vs 82.4-82.8)
+  static constexpr bool kDownPair = ENC == kQ4 && NMAT == 1 && NB == 1 && KW == 1 && MW == 8;
+  static constexpr int D = kDownPair ? 4
+                                     : (BUF <= 12 * 1024 ? 6
+                                                         : (BUF <= 24 * 1024 || (BUF <= 32 * 1024 && NB != 3) ? 4 : 3));
   static constexpr int NL = (D - 2) * I_STEP > 63 ? 2 : 1;  // loader waves
   static constexpr int I_WAVE = I_STEP / NL;
   static constexpr int THREADS = 64 * (MW + NL);
