@@ -242,20 +242,24 @@ struct MfmaCfg {
   static constexpr int X_INSTR = X_BYTES / 1024;
   static constexpr int I_STEP = W_INSTR + X_INSTR;
   // ring depth: 48-route gate/up tiles (28 KB steps) keep 3 buffers so that
-  // the ring, three scale slots and the metadata fit the 160 KB of LDS; the
-  // Q4 down projection's 16-route tiles (12 KB steps) keep 4, so that two
-  // workgroups (two loader waves) share a CU (batch 32 100.6-100.8 vs
-  // 102.3-102.5 us per call with 6, T = 16 80.0-80.3 vs 82.4-82.8)
+  // the ring, three scale slots and the metadata fit the 160 KB of LDS. The
+  // Q4 down projection keeps two workgroups (two loader waves) per CU: its
+  // 16-route tiles (12 KB steps) with 4 buffers (batch 32 100.6-100.8 vs
+  // 102.3-102.5 us per call with 6, T = 16 80.0-80.3 vs 82.4-82.8), its
+  // 48-route tiles (20 KB steps) with 3 buffers and two scale slots (c4
+  // 166.7-167.2 vs 169.6-170.2 us with 4 buffers and three slots)
   static constexpr bool kDownPair = ENC == kQ4 && NMAT == 1 && NB == 1 && KW == 1 && MW == 8;
+  static constexpr bool kDown48Pair = ENC == kQ4 && NMAT == 1 && NB == 3 && KW == 1 && MW == 8;
   static constexpr int D = kDownPair ? 4
-                                     : (BUF <= 12 * 1024 ? 6
-                                                         : (BUF <= 24 * 1024 || (BUF <= 32 * 1024 && NB != 3) ? 4 : 3));
+                                     : (kDown48Pair ? 3 : (BUF <= 12 * 1024 ? 6
+                                                         : (BUF <= 24 * 1024 || (BUF <= 32 * 1024 && NB != 3) ? 4 : 3)));
   static constexpr int NL = (D - 2) * I_STEP > 63 ? 2 : 1;  // loader waves
   static constexpr int I_WAVE = I_STEP / NL;
   static constexpr int THREADS = 64 * (MW + NL);
   // item slots for the scales: 2 for the wide Q4 gate/up tiles (40 KB steps),
-  // whose ring and three slots would not fit the LDS
-  static constexpr int SLOTS = ENC == kQ4Wide && NMAT == 2 ? 2 : 3;
+  // whose ring and three slots would not fit the LDS, and for the Q4 down
+  // projection's 48-route tiles (two workgroups per CU)
+  static constexpr int SLOTS = (ENC == kQ4Wide && NMAT == 2) || kDown48Pair ? 2 : 3;
   static constexpr int MAX_ITEMS = NTOK <= 32 ? 32 : 16;  // work items per workgroup
   static constexpr int META = 4 + NTOK;                // expert, first route, routes, row block, route ids
   static constexpr int RED_BYTES = KW > 1 ? (KW - 1) * WR * AT * NB * 4 * 64 * 4 : 0;
